@@ -1,0 +1,22 @@
+"""csrspmm_amd: CSR sparse x dense matrix multiplication for AMD Instinct
+MI355X (gfx950), C = alpha * A * B + beta * C with A in CSR (int32 indices,
+fp32 values) and row-major fp32 B and C.
+
+Surfaces:
+  include/csrspmm_c.h         C ABI (libcsrspmm_hip.so: kernels + launch)
+  include/csrspmm/*.h         drop-in C++ API of the reference (libcsrspmm.so)
+  csrspmm_amd.torch_csrspmm   drop-in torch entry points (torch_csrspmm/_C)
+  csrspmm_amd.capi            ctypes view of the C ABI (tests, benchmarks)
+  csrspmm_amd.gen / configs   seeded synthetic inputs and the benchmark configs
+"""
+import os
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_DIR = os.path.join(PKG_DIR, "lib")
+
+ALGORITHMS = ("Naive", "NaiveSmem", "WarpPerRow", "WarpPerRowFp4", "WarpPerRowSmem",
+              "WarpPerRowSmemFp4")
+# The five variants the reference's torch package exposes (torch_csrspmm/__init__.py:10-23).
+TORCH_ALGORITHMS = ("Naive", "WarpPerRow", "WarpPerRowSmem", "WarpPerRowFp4", "WarpPerRowSmemFp4")
+
+__version__ = "0.1.0"

@@ -1,0 +1,175 @@
+"""ctypes view of the C ABI (include/csrspmm_c.h, include/csrspmm_gen.h).
+
+Loading imports torch first so that libcsrspmm_hip.so binds to the HIP
+runtime torch already loaded (both are SONAME libamdhip64.so.7): one runtime
+per process, so torch's device pointers and streams are valid here.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (see module docstring)
+
+from . import LIB_DIR
+
+_c_int, _c_ll, _c_float, _c_void_p, _c_size_t = (ctypes.c_int, ctypes.c_longlong, ctypes.c_float,
+                                                 ctypes.c_void_p, ctypes.c_size_t)
+_c_u64 = ctypes.c_uint64
+
+ALGO = {"Naive": 0, "NaiveSmem": 1, "WarpPerRow": 2, "WarpPerRowFp4": 3, "WarpPerRowSmem": 4,
+        "WarpPerRowSmemFp4": 5}
+FLAG_C_IS_ZERO = 1
+
+# Every function include/csrspmm_c.h declares: name -> (restype, argtypes).
+HIP_API = {
+    "csrspmm_version": (_c_int, []),
+    "csrspmm_status_string": (ctypes.c_char_p, [_c_int]),
+    "csrspmm_parse_algorithm": (_c_int, [ctypes.c_char_p]),
+    "csrspmm_algorithm_name": (ctypes.c_char_p, [_c_int]),
+    "csrspmm_workspace_bytes": (_c_size_t, [_c_int, _c_int, _c_int, _c_int]),
+    "csrspmm_spmm_f32": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p, _c_void_p,
+                                  _c_void_p, _c_int, _c_void_p, _c_ll, _c_void_p, _c_ll, _c_float,
+                                  _c_float, _c_void_p]),
+    "csrspmm_spmm_f32_ex": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p, _c_void_p,
+                                     _c_void_p, _c_int, _c_void_p, _c_ll, _c_void_p, _c_ll,
+                                     _c_float, _c_float, ctypes.c_uint, _c_void_p, _c_size_t,
+                                     _c_void_p]),
+    "csrspmm_validate_csr": (_c_int, [_c_int, _c_int, _c_int, _c_void_p, _c_void_p,
+                                      ctypes.POINTER(_c_int), ctypes.POINTER(_c_int), _c_void_p]),
+    "csrspmm_device_malloc": (_c_int, [ctypes.POINTER(_c_void_p), _c_size_t]),
+    "csrspmm_device_free": (_c_int, [_c_void_p]),
+    "csrspmm_memcpy_h2d": (_c_int, [_c_void_p, _c_void_p, _c_size_t]),
+    "csrspmm_memcpy_d2h": (_c_int, [_c_void_p, _c_void_p, _c_size_t]),
+    "csrspmm_memcpy_d2d": (_c_int, [_c_void_p, _c_void_p, _c_size_t, _c_void_p]),
+    "csrspmm_device_synchronize": (_c_int, []),
+    "csrspmm_stream_synchronize": (_c_int, [_c_void_p]),
+    "csrspmm_get_last_error": (_c_int, []),
+    "csrspmm_device_count": (_c_int, []),
+    "csrspmm_timing_enable": (_c_int, [_c_int]),
+    "csrspmm_timing_read": (_c_int, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_c_int)]),
+}
+
+# Every function include/csrspmm_gen.h declares.
+GEN_API = {
+    "csrspmm_gen_key": (_c_u64, [_c_u64, _c_int]),
+    "csrspmm_gen_rand": (_c_u64, [_c_u64, _c_u64]),
+    "csrspmm_gen_dense": (None, [_c_u64, _c_int, _c_u64, _c_size_t, _c_void_p]),
+    "csrspmm_gen_uniform": (_c_void_p, [_c_int, _c_int, _c_int, _c_u64]),
+    "csrspmm_gen_powerlaw": (_c_void_p, [_c_int, _c_int, ctypes.c_double, ctypes.c_double, _c_int,
+                                         _c_u64]),
+    "csrspmm_gen_ragged": (_c_void_p, [_c_int, _c_int, _c_int, _c_int, _c_u64]),
+    "csrspmm_gen_rmat": (_c_void_p, [_c_int, _c_ll, ctypes.c_double, ctypes.c_double,
+                                     ctypes.c_double, _c_u64]),
+    "csrspmm_gen_shape": (_c_int, [_c_void_p, ctypes.POINTER(_c_int), ctypes.POINTER(_c_int),
+                                   ctypes.POINTER(_c_ll), ctypes.POINTER(_c_int)]),
+    "csrspmm_gen_copy": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p]),
+    "csrspmm_gen_free": (None, [_c_void_p]),
+    "csrspmm_fnv1a64": (_c_u64, [_c_u64, _c_void_p, _c_size_t]),
+}
+
+_hip = None
+_host = None
+
+
+def _bind(lib, table):
+    for name, (res, args) in table.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+def _load(name):
+    path = os.path.join(LIB_DIR, name)
+    if not os.path.exists(path):
+        raise OSError(f"{path} is missing: build it with `python -m csrspmm_amd.build`")
+    return ctypes.CDLL(path, mode=ctypes.RTLD_GLOBAL)
+
+
+def hip():
+    """libcsrspmm_hip.so with the C ABI bound."""
+    global _hip
+    if _hip is None:
+        _hip = _bind(_load("libcsrspmm_hip.so"), HIP_API)
+    return _hip
+
+
+def host():
+    """libcsrspmm.so (C++ API + generators) with the generator ABI bound."""
+    global _host
+    if _host is None:
+        hip()
+        _host = _bind(_load("libcsrspmm.so"), GEN_API)
+    return _host
+
+
+class CsrspmmError(RuntimeError):
+    def __init__(self, status: int, what: str = ""):
+        msg = hip().csrspmm_status_string(status).decode()
+        super().__init__(f"{what}: status {status} ({msg})" if what else f"status {status} ({msg})")
+        self.status = status
+
+
+def check(status: int, what: str = "") -> None:
+    if status != 0:
+        raise CsrspmmError(status, what)
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def spmm(algo, rowptr, colidx, vals, B, C, alpha, beta, *, M=None, K=None, hint=-1, flags=0,
+         workspace=None, stream=None, owned_workspace=False):
+    """C = alpha*A*B + beta*C through csrspmm_spmm_f32_ex (or csrspmm_spmm_f32
+    when owned_workspace=True).  All tensors on one GPU; C is written in place.
+    Returns C.  Allocates the workspace with torch when none is given."""
+    a = ALGO[algo] if isinstance(algo, str) else int(algo)
+    M = rowptr.numel() - 1 if M is None else M
+    K = B.shape[0] if K is None else K
+    N = C.shape[1]
+    nnz = vals.numel()
+    ldb = B.stride(0) if B.dim() == 2 and B.shape[1] > 1 else max(N, 1)
+    ldc = C.stride(0) if C.shape[1] > 1 else max(N, 1)
+    if stream is None:
+        stream = torch.cuda.current_stream(C.device).cuda_stream
+    lib = hip()
+    if owned_workspace:
+        st = lib.csrspmm_spmm_f32(a, M, K, N, nnz, _ptr(rowptr), _ptr(colidx), _ptr(vals), hint,
+                                  _ptr(B), ldb, _ptr(C), ldc, alpha, beta, ctypes.c_void_p(stream))
+    else:
+        need = lib.csrspmm_workspace_bytes(a, M, N, nnz)
+        if workspace is None and need > 0:
+            workspace = torch.empty(need, dtype=torch.uint8, device=C.device)
+        wsz = 0 if workspace is None else workspace.numel()
+        st = lib.csrspmm_spmm_f32_ex(a, M, K, N, nnz, _ptr(rowptr), _ptr(colidx), _ptr(vals),
+                                     hint, _ptr(B), ldb, _ptr(C), ldc, alpha, beta, flags,
+                                     _ptr(workspace), wsz, ctypes.c_void_p(stream))
+    check(st, f"csrspmm_spmm {algo}")
+    return C
+
+
+def timing_enable(on: bool) -> None:
+    check(hip().csrspmm_timing_enable(1 if on else 0), "csrspmm_timing_enable")
+
+
+def timing_read():
+    """(summed main-kernel ms, calls) since the previous read."""
+    ms = ctypes.c_double(0.0)
+    n = _c_int(0)
+    check(hip().csrspmm_timing_read(ctypes.byref(ms), ctypes.byref(n)), "csrspmm_timing_read")
+    return ms.value, n.value
+
+
+def validate(rowptr, colidx, K, stream=None):
+    """(flags, max_row_nnz) from the device validator."""
+    M = rowptr.numel() - 1
+    f = _c_int(0)
+    m = _c_int(0)
+    if stream is None:
+        stream = torch.cuda.current_stream(rowptr.device).cuda_stream
+    check(hip().csrspmm_validate_csr(M, K, colidx.numel(), _ptr(rowptr), _ptr(colidx),
+                                     ctypes.byref(f), ctypes.byref(m), ctypes.c_void_p(stream)),
+          "csrspmm_validate_csr")
+    return f.value, m.value

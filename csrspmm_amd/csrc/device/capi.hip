@@ -1,0 +1,393 @@
+// C ABI (include/csrspmm_c.h) over the gfx950 kernels: argument checks,
+// variant dispatch, workspace management, CSR validation and the memory
+// helpers the g++-built C++ layer uses.
+
+#include <hip/hip_runtime.h>
+
+#include <map>
+#include <mutex>
+#include <string.h>
+#include <utility>
+#include <vector>
+
+#include "../../../include/csrspmm_c.h"
+#include "common.hpp"
+#include "spmm_internal.h"
+
+namespace csrspmm_hip {
+
+static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+WorkspaceLayout workspace_layout(int M, int N, int nnz) {
+  WorkspaceLayout L{};
+  const long long long_cap = std::min<long long>(M, (long long)nnz / (kSplitLen + 1));
+  const long long seg_cap = (long long)nnz / kSplitLen + 1 + long_cap;
+  L.long_cap = (int)long_cap;
+  L.seg_cap = (int)seg_cap;
+  L.ldp = ((long long)N + 3) & ~3LL;
+  size_t off = 0;
+  L.counters_off = off;
+  off = align256(off + 4 * sizeof(int));
+  L.seg_info_off = off;
+  off = align256(off + (size_t)seg_cap * sizeof(int2));
+  L.long_rows_off = off;
+  off = align256(off + (size_t)long_cap * sizeof(int4));
+  L.partials_off = off;
+  off = align256(off + (size_t)seg_cap * (size_t)L.ldp * sizeof(float));
+  L.total = off;
+  return L;
+}
+
+void bind_workspace(Problem& p, void* ws, const WorkspaceLayout& L) {
+  char* b = static_cast<char*>(ws);
+  p.counters = reinterpret_cast<int*>(b + L.counters_off);
+  p.seg_info = reinterpret_cast<int2*>(b + L.seg_info_off);
+  p.long_rows = reinterpret_cast<int4*>(b + L.long_rows_off);
+  p.partials = reinterpret_cast<float*>(b + L.partials_off);
+  p.ldp = L.ldp;
+  p.seg_cap = L.seg_cap;
+  p.long_cap = L.long_cap;
+}
+
+namespace {
+
+bool is_rowgroup(int algo) {
+  return algo == CSRSPMM_ALGO_WARP_PER_ROW || algo == CSRSPMM_ALGO_WARP_PER_ROW_FP4 ||
+         algo == CSRSPMM_ALGO_WARP_PER_ROW_SMEM || algo == CSRSPMM_ALGO_WARP_PER_ROW_SMEM_FP4;
+}
+
+bool wants_plan(int algo, int hint) {
+  return is_rowgroup(algo) && (hint < 0 || hint > kSplitLen);
+}
+
+int to_status(hipError_t e) { return e == hipSuccess ? 0 : (int)e; }
+
+struct OwnedWorkspace {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+};
+
+std::mutex g_ws_mutex;
+std::map<std::pair<int, void*>, OwnedWorkspace> g_ws;
+
+// Grow-only workspace per (device, stream).  Growing waits for the stream so
+// the old buffer is no longer in use when it is freed.
+int owned_workspace(void* stream, size_t bytes, void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  std::lock_guard<std::mutex> lock(g_ws_mutex);
+  OwnedWorkspace& w = g_ws[std::make_pair(dev, stream)];
+  if (w.bytes < bytes) {
+    if (w.ptr) {
+      e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+      if (e != hipSuccess) return (int)e;
+      e = hipFree(w.ptr);
+      w.ptr = nullptr;
+      w.bytes = 0;
+      if (e != hipSuccess) return (int)e;
+    }
+    const size_t want = bytes + bytes / 4;  // headroom against repeated small growth
+    e = hipMalloc(&w.ptr, want);
+    if (e != hipSuccess) {
+      w.ptr = nullptr;
+      (void)hipGetLastError();
+      return CSRSPMM_STATUS_ALLOC_FAILED;
+    }
+    w.bytes = want;
+  }
+  *out = w.ptr;
+  return 0;
+}
+
+int check_args(int algo, int M, int K, int N, int nnz, const int* rowptr, const int* colidx,
+               const float* vals, const float* B, long long ldb, const float* C, long long ldc) {
+  if (algo < 0 || algo >= CSRSPMM_ALGO_COUNT) return CSRSPMM_STATUS_INVALID_VALUE;
+  if (M < 0 || K < 0 || N < 0 || nnz < 0) return CSRSPMM_STATUS_INVALID_VALUE;
+  if (M == 0 || N == 0) return 0;
+  if (!rowptr || !C) return CSRSPMM_STATUS_INVALID_VALUE;
+  if (nnz > 0 && (!colidx || !vals || !B || K == 0)) return CSRSPMM_STATUS_INVALID_VALUE;
+  if (ldc < N || (nnz > 0 && ldb < N)) return CSRSPMM_STATUS_INVALID_VALUE;
+  // 64-bit offsets are used for B and C; the grid and row indices are 32-bit.
+  if ((long long)M * 64 > 0x7fffffffLL * 64LL) return CSRSPMM_STATUS_NOT_SUPPORTED;
+  return 0;
+}
+
+int spmm_impl(int algo, int M, int K, int N, int nnz, const int* rowptr, const int* colidx,
+              const float* vals, int hint, const float* B, long long ldb, float* C, long long ldc,
+              float alpha, float beta, unsigned flags, void* ws, size_t ws_bytes, bool owned,
+              void* stream) {
+  int st = check_args(algo, M, K, N, nnz, rowptr, colidx, vals, B, ldb, C, ldc);
+  if (st != 0) return st;
+  if (M == 0 || N == 0) return 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+
+  Problem p{};
+  p.M = M;
+  p.K = K;
+  p.N = N;
+  p.nnz = nnz;
+  p.rowptr = rowptr;
+  p.colidx = colidx;
+  p.vals = vals;
+  p.B = B;
+  p.ldb = ldb;
+  p.C = C;
+  p.ldc = ldc;
+  p.alpha = alpha;
+  p.beta = beta;
+  if (flags & 1u)
+    p.epi = kEpiZeroC;
+  else
+    p.epi = (beta == 0.0f) ? kEpiOverwrite : kEpiAccumulate;
+  p.plan = wants_plan(algo, hint) && nnz > kSplitLen;
+
+  if (p.plan) {
+    const WorkspaceLayout L = workspace_layout(M, N, nnz);
+    if (owned) {
+      st = owned_workspace(stream, L.total, &ws);
+      if (st != 0) return st;
+    } else {
+      if (!ws || ws_bytes < L.total) return CSRSPMM_STATUS_WORKSPACE_TOO_SMALL;
+      if (reinterpret_cast<uintptr_t>(ws) & 255) return CSRSPMM_STATUS_INVALID_VALUE;
+    }
+    bind_workspace(p, ws, L);
+  }
+
+  // The float4 forms need 16-byte aligned rows of B and C; otherwise the
+  // scalar-column kernel of the same family runs (the reference instead drops
+  // the last N % 4 columns, csrspmm_warp_per_row_fp4.cu:29-32).
+  const bool vec_ok = (N % 4 == 0) && (ldc % 4 == 0) &&
+                      ((reinterpret_cast<uintptr_t>(C) & 15) == 0) &&
+                      (nnz == 0 || ((ldb % 4 == 0) && ((reinterpret_cast<uintptr_t>(B) & 15) == 0)));
+  hipError_t e = hipSuccess;
+  switch (algo) {
+    case CSRSPMM_ALGO_NAIVE: e = launch_naive(p, s); break;
+    case CSRSPMM_ALGO_NAIVE_SMEM: e = launch_naive_smem(p, s); break;
+    case CSRSPMM_ALGO_WARP_PER_ROW: e = launch_rowgroup(p, 1, false, s); break;
+    case CSRSPMM_ALGO_WARP_PER_ROW_FP4: e = launch_rowgroup(p, vec_ok ? 4 : 1, false, s); break;
+    case CSRSPMM_ALGO_WARP_PER_ROW_SMEM: e = launch_rowgroup(p, 1, true, s); break;
+    case CSRSPMM_ALGO_WARP_PER_ROW_SMEM_FP4: e = launch_rowgroup(p, vec_ok ? 4 : 1, true, s); break;
+    default: return CSRSPMM_STATUS_INVALID_VALUE;
+  }
+  return to_status(e);
+}
+
+// One wave per row: rowptr monotonicity and row length (lane 0), column
+// range and in-row order (all lanes).  Reads are clamped to [0, nnz) so a
+// malformed rowptr cannot send the validator out of bounds.
+__global__ __launch_bounds__(256) void validate_kernel(int M, int K, int nnz, const int* rowptr,
+                                                       const int* colidx, int* out) {
+  __shared__ int s_flags;
+  __shared__ int s_max;
+  if (threadIdx.x == 0) {
+    s_flags = 0;
+    s_max = 0;
+  }
+  __syncthreads();
+  const int lane = lane_id();
+  const int nw = blockDim.x >> 6;
+  int flags = 0;
+  int mx = 0;
+  for (int row = blockIdx.x * nw + (threadIdx.x >> 6); row < M; row += gridDim.x * nw) {
+    const int rs = rowptr[row];
+    const int re = rowptr[row + 1];
+    if (lane == 0) {
+      if (re < rs) flags |= CSRSPMM_CSR_NON_MONOTONE;
+      mx = max(mx, re - rs);
+      if (row == 0 && rs != 0) flags |= CSRSPMM_CSR_BAD_ROWPTR0;
+      if (row == M - 1 && re != nnz) flags |= CSRSPMM_CSR_BAD_ROWPTR_END;
+    }
+    const int lo = max(rs, 0);
+    const int hi = min(re, nnz);
+    for (int j = lo + lane; j < hi; j += 64) {
+      const int c = colidx[j];
+      if (c < 0 || c >= K) flags |= CSRSPMM_CSR_COL_OUT_OF_RANGE;
+      if (j + 1 < hi && colidx[j + 1] <= c) flags |= CSRSPMM_CSR_UNSORTED;
+    }
+  }
+  if (flags) atomicOr(&s_flags, flags);
+  if (mx) atomicMax(&s_max, mx);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    if (s_flags) atomicOr(&out[0], s_flags);
+    atomicMax(&out[1], s_max);
+  }
+}
+
+__global__ void zero2_kernel(int* out) {
+  if (threadIdx.x < 2) out[threadIdx.x] = 0;
+}
+
+// Timing hook state: a pool of event pairs; pairs [0, g_t_used) hold
+// recordings not yet read.
+std::mutex g_t_mutex;
+bool g_t_on = false;
+std::vector<std::pair<hipEvent_t, hipEvent_t>> g_t_events;
+size_t g_t_used = 0;
+
+}  // namespace
+
+void timing_before_main(hipStream_t s) {
+  std::lock_guard<std::mutex> lock(g_t_mutex);
+  if (!g_t_on) return;
+  if (g_t_used == g_t_events.size()) {
+    hipEvent_t a, b;
+    if (hipEventCreate(&a) != hipSuccess) return;
+    if (hipEventCreate(&b) != hipSuccess) {
+      (void)hipEventDestroy(a);
+      return;
+    }
+    g_t_events.emplace_back(a, b);
+  }
+  (void)hipEventRecord(g_t_events[g_t_used].first, s);
+}
+
+void timing_after_main(hipStream_t s) {
+  std::lock_guard<std::mutex> lock(g_t_mutex);
+  if (!g_t_on || g_t_used == g_t_events.size()) return;
+  (void)hipEventRecord(g_t_events[g_t_used].second, s);
+  ++g_t_used;
+}
+
+hipError_t launch_validate(int M, int K, int nnz, const int* rowptr, const int* colidx, int* d_out,
+                           hipStream_t s) {
+  hipLaunchKernelGGL(zero2_kernel, dim3(1), dim3(64), 0, s, d_out);
+  if (M > 0) {
+    const int blocks = std::min(div_up_host(M, 4), 65536);
+    hipLaunchKernelGGL(validate_kernel, dim3(blocks), dim3(256), 0, s, M, K, nnz, rowptr, colidx, d_out);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace csrspmm_hip
+
+using namespace csrspmm_hip;
+
+extern "C" {
+
+int csrspmm_version(void) { return 100; }
+
+const char* csrspmm_status_string(int status) {
+  switch (status) {
+    case CSRSPMM_STATUS_SUCCESS: return "success";
+    case CSRSPMM_STATUS_INVALID_VALUE: return "invalid value";
+    case CSRSPMM_STATUS_NOT_SUPPORTED: return "not supported";
+    case CSRSPMM_STATUS_ALLOC_FAILED: return "workspace allocation failed";
+    case CSRSPMM_STATUS_INVALID_CSR: return "invalid CSR matrix";
+    case CSRSPMM_STATUS_WORKSPACE_TOO_SMALL: return "workspace too small";
+    default:
+      if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));
+      return "unknown status";
+  }
+}
+
+static const char* const kAlgoNames[CSRSPMM_ALGO_COUNT] = {
+    "Naive", "NaiveSmem", "WarpPerRow", "WarpPerRowFp4", "WarpPerRowSmem", "WarpPerRowSmemFp4"};
+
+int csrspmm_parse_algorithm(const char* name) {
+  if (!name) return -1;
+  for (int i = 0; i < CSRSPMM_ALGO_COUNT; ++i)
+    if (strcmp(name, kAlgoNames[i]) == 0) return i;
+  return -1;
+}
+
+const char* csrspmm_algorithm_name(int algo) {
+  if (algo < 0 || algo >= CSRSPMM_ALGO_COUNT) return nullptr;
+  return kAlgoNames[algo];
+}
+
+size_t csrspmm_workspace_bytes(int algo, int M, int N, int nnz) {
+  if (!is_rowgroup(algo) || M <= 0 || N <= 0 || nnz <= kSplitLen) return 0;
+  return workspace_layout(M, N, nnz).total;
+}
+
+int csrspmm_spmm_f32(int algo, int M, int K, int N, int nnz, const int* rowptr, const int* colidx,
+                     const float* vals, int max_row_nnz_hint, const float* B, long long ldb, float* C,
+                     long long ldc, float alpha, float beta, void* stream) {
+  return spmm_impl(algo, M, K, N, nnz, rowptr, colidx, vals, max_row_nnz_hint, B, ldb, C, ldc, alpha,
+                   beta, 0u, nullptr, 0, true, stream);
+}
+
+int csrspmm_spmm_f32_ex(int algo, int M, int K, int N, int nnz, const int* rowptr, const int* colidx,
+                        const float* vals, int max_row_nnz_hint, const float* B, long long ldb,
+                        float* C, long long ldc, float alpha, float beta, unsigned flags,
+                        void* workspace, size_t workspace_bytes, void* stream) {
+  return spmm_impl(algo, M, K, N, nnz, rowptr, colidx, vals, max_row_nnz_hint, B, ldb, C, ldc, alpha,
+                   beta, flags, workspace, workspace_bytes, false, stream);
+}
+
+int csrspmm_validate_csr(int M, int K, int nnz, const int* rowptr, const int* colidx, int* flags_out,
+                         int* max_row_nnz_out, void* stream) {
+  if (M < 0 || K < 0 || nnz < 0 || (!rowptr && M > 0) || (!colidx && nnz > 0))
+    return CSRSPMM_STATUS_INVALID_VALUE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int* d_out = nullptr;
+  hipError_t e = hipMalloc(&d_out, 2 * sizeof(int));
+  if (e != hipSuccess) return (int)e;
+  int h_out[2] = {0, 0};
+  e = launch_validate(M, K, nnz, rowptr, colidx, d_out, s);
+  if (e == hipSuccess) e = hipMemcpyAsync(h_out, d_out, sizeof(h_out), hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  hipError_t e2 = hipFree(d_out);
+  if (e != hipSuccess) return (int)e;
+  if (e2 != hipSuccess) return (int)e2;
+  if (M == 0 && nnz != 0) h_out[0] |= CSRSPMM_CSR_BAD_ROWPTR_END;
+  if (flags_out) *flags_out = h_out[0];
+  if (max_row_nnz_out) *max_row_nnz_out = h_out[1];
+  return 0;
+}
+
+int csrspmm_device_malloc(void** ptr, size_t bytes) {
+  if (!ptr) return CSRSPMM_STATUS_INVALID_VALUE;
+  return to_status(hipMalloc(ptr, bytes));
+}
+int csrspmm_device_free(void* ptr) { return to_status(hipFree(ptr)); }
+int csrspmm_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+  return to_status(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+}
+int csrspmm_memcpy_d2h(void* dst, const void* src, size_t bytes) {
+  return to_status(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+}
+int csrspmm_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream) {
+  return to_status(
+      hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, static_cast<hipStream_t>(stream)));
+}
+int csrspmm_device_synchronize(void) { return to_status(hipDeviceSynchronize()); }
+int csrspmm_stream_synchronize(void* stream) {
+  return to_status(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+}
+int csrspmm_get_last_error(void) { return to_status(hipGetLastError()); }
+int csrspmm_timing_enable(int on) {
+  std::lock_guard<std::mutex> lock(g_t_mutex);
+  g_t_on = on != 0;
+  return 0;
+}
+
+int csrspmm_timing_read(double* main_kernel_ms, int* calls) {
+  std::lock_guard<std::mutex> lock(g_t_mutex);
+  double total = 0.0;
+  for (size_t i = 0; i < g_t_used; ++i) {
+    hipError_t e = hipEventSynchronize(g_t_events[i].second);
+    if (e != hipSuccess) return (int)e;
+    float ms = 0.0f;
+    e = hipEventElapsedTime(&ms, g_t_events[i].first, g_t_events[i].second);
+    if (e != hipSuccess) return (int)e;
+    total += ms;
+  }
+  if (main_kernel_ms) *main_kernel_ms = total;
+  if (calls) *calls = (int)g_t_used;
+  g_t_used = 0;
+  return 0;
+}
+
+int csrspmm_device_count(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return n;
+}
+
+}  // extern "C"

@@ -1,0 +1,100 @@
+// Device helpers shared by the gfx950 SpMM kernels (wave64, CDNA4).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <algorithm>
+
+#include "spmm_internal.h"
+
+namespace csrspmm_hip {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+template <int VEC> struct Vec;
+template <> struct Vec<1> {
+  using T = float;
+  static __device__ __forceinline__ T zero() { return 0.0f; }
+};
+template <> struct Vec<4> {
+  using T = f4;
+  static __device__ __forceinline__ T zero() { return f4{0.0f, 0.0f, 0.0f, 0.0f}; }
+};
+
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+// A (colidx, values) is streamed exactly once: load it non-temporally so it
+// does not push gathered B rows out of L2 / the MALL.
+__device__ __forceinline__ int ld_stream(const int* p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ float ld_stream(const float* p) { return __builtin_nontemporal_load(p); }
+
+// B rows are gathered (reused across rows that share a column): normal cached loads.
+template <int VEC>
+__device__ __forceinline__ typename Vec<VEC>::T ld_b(const float* p) {
+  return *reinterpret_cast<const typename Vec<VEC>::T*>(p);
+}
+
+// C is written once: non-temporal stores keep it out of the caches B lives in.
+__device__ __forceinline__ void st_c(float* p, float v) { __builtin_nontemporal_store(v, p); }
+__device__ __forceinline__ void st_c(float* p, f4 v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<f4*>(p));
+}
+
+__device__ __forceinline__ float fmaf_(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
+__device__ __forceinline__ f4 fma4(float a, f4 b, f4 c) {
+  return f4{__builtin_fmaf(a, b.x, c.x), __builtin_fmaf(a, b.y, c.y),
+            __builtin_fmaf(a, b.z, c.z), __builtin_fmaf(a, b.w, c.w)};
+}
+__device__ __forceinline__ float fma_v(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
+__device__ __forceinline__ f4 fma_v(float a, f4 b, f4 c) { return fma4(a, b, c); }
+
+__device__ __forceinline__ float add_v(float a, float b) { return a + b; }
+__device__ __forceinline__ f4 add_v(f4 a, f4 b) { return a + b; }
+
+// Epilogue, per element: out = alpha*sum (+ beta*c0).  Written with an
+// explicit fma so the rounding does not depend on compiler contraction.
+__device__ __forceinline__ float epi1(int mode, float alpha, float beta, float sum, const float* cptr) {
+  if (mode == kEpiOverwrite) return alpha * sum;
+  const float c0 = (mode == kEpiAccumulate) ? *cptr : 0.0f;
+  return __builtin_fmaf(alpha, sum, beta * c0);
+}
+
+__device__ __forceinline__ f4 epi4(int mode, float alpha, float beta, f4 sum, const float* cptr) {
+  if (mode == kEpiOverwrite) return f4{alpha * sum.x, alpha * sum.y, alpha * sum.z, alpha * sum.w};
+  f4 c0 = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  if (mode == kEpiAccumulate) c0 = *reinterpret_cast<const f4*>(cptr);
+  return f4{__builtin_fmaf(alpha, sum.x, beta * c0.x), __builtin_fmaf(alpha, sum.y, beta * c0.y),
+            __builtin_fmaf(alpha, sum.z, beta * c0.z), __builtin_fmaf(alpha, sum.w, beta * c0.w)};
+}
+
+template <int VEC>
+__device__ __forceinline__ void store_epi(const Problem& p, float* cptr, typename Vec<VEC>::T sum) {
+  if constexpr (VEC == 1) {
+    st_c(cptr, epi1(p.epi, p.alpha, p.beta, sum, cptr));
+  } else {
+    st_c(cptr, epi4(p.epi, p.alpha, p.beta, sum, cptr));
+  }
+}
+
+// Broadcast lane (gbase + k) of a G-lane group to the whole group.  For a
+// full-wave group the source lane is wave-uniform, so v_readlane puts the
+// value in an SGPR (B row address becomes scalar base + per-lane offset);
+// smaller groups use ds_bpermute (LDS crossbar, no LDS storage).
+template <int G>
+__device__ __forceinline__ int group_bcast(int v, int gbase, int k) {
+  if constexpr (G == 64) {
+    return __builtin_amdgcn_readlane(v, k);
+  } else {
+    return __builtin_amdgcn_ds_bpermute((gbase + k) << 2, v);
+  }
+}
+template <int G>
+__device__ __forceinline__ float group_bcast(float v, int gbase, int k) {
+  return __builtin_bit_cast(float, group_bcast<G>(__builtin_bit_cast(int, v), gbase, k));
+}
+
+__device__ __forceinline__ int div_up(int a, int b) { return (a + b - 1) / b; }
+static inline int div_up_host(int a, int b) { return (a + b - 1) / b; }
+
+}  // namespace csrspmm_hip

@@ -1,0 +1,171 @@
+/*
+ * csrspmm_c.h -- the C ABI of the MI355X (gfx950) CSR SpMM library.
+ *
+ * Computes C = alpha * A * B + beta * C for A in CSR (int32 indices, fp32
+ * values, M x K, nnz nonzeros) and dense row-major fp32 B (K x N, leading
+ * dimension ldb) and C (M x N, leading dimension ldc).  When beta == 0 the
+ * prior contents of C are never read (NaN in C is overwritten).
+ *
+ * Every entry point takes plain pointers and sizes, no C++ or torch types.
+ * Device pointers are caller-owned; the library never frees user memory.
+ * Status convention: 0 = success, negative = CSRSPMM_STATUS_* below,
+ * positive = a hipError_t value reported by the HIP runtime.
+ *
+ * This header is the only surface through which host C++ (libcsrspmm.so,
+ * built with g++), the torch extension and ctypes reach HIP.  Each entry
+ * point names the reference interface it replaces (anh-thh/csrspmm paths).
+ */
+#ifndef CSRSPMM_C_H_
+#define CSRSPMM_C_H_
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Algorithm ids, in the order of csrspmm::Algorithm
+ * (reference include/csrspmm/csrspmm.h:10-17). */
+enum {
+    CSRSPMM_ALGO_NAIVE = 0,
+    CSRSPMM_ALGO_NAIVE_SMEM = 1,
+    CSRSPMM_ALGO_WARP_PER_ROW = 2,
+    CSRSPMM_ALGO_WARP_PER_ROW_FP4 = 3,
+    CSRSPMM_ALGO_WARP_PER_ROW_SMEM = 4,
+    CSRSPMM_ALGO_WARP_PER_ROW_SMEM_FP4 = 5,
+    CSRSPMM_ALGO_COUNT = 6
+};
+
+enum {
+    CSRSPMM_STATUS_SUCCESS = 0,
+    CSRSPMM_STATUS_INVALID_VALUE = -1,     /* bad size, null pointer, bad ld, unknown algo */
+    CSRSPMM_STATUS_NOT_SUPPORTED = -2,     /* shape beyond int32 index range */
+    CSRSPMM_STATUS_ALLOC_FAILED = -3,      /* library-owned workspace could not grow */
+    CSRSPMM_STATUS_INVALID_CSR = -4,       /* validator found a malformed CSR */
+    CSRSPMM_STATUS_WORKSPACE_TOO_SMALL = -5
+};
+
+/* Validator result bits (csrspmm_validate_csr). */
+enum {
+    CSRSPMM_CSR_OK = 0,
+    CSRSPMM_CSR_BAD_ROWPTR0 = 1,       /* rowptr[0] != 0 */
+    CSRSPMM_CSR_BAD_ROWPTR_END = 2,    /* rowptr[M] != nnz */
+    CSRSPMM_CSR_NON_MONOTONE = 4,      /* rowptr[i+1] < rowptr[i] for some i */
+    CSRSPMM_CSR_COL_OUT_OF_RANGE = 8,  /* col < 0 or col >= K */
+    CSRSPMM_CSR_UNSORTED = 16,         /* informational: columns not strictly increasing in a row */
+    CSRSPMM_CSR_FATAL_MASK = 15        /* bits that make a kernel launch unsafe */
+};
+
+/* Library version as 10000*major + 100*minor + patch. */
+int csrspmm_version(void);
+
+/* Human-readable text for a status code (never NULL). */
+const char* csrspmm_status_string(int status);
+
+/* Name -> algorithm id by exact CamelCase match ("Naive", "NaiveSmem",
+ * "WarpPerRow", "WarpPerRowFp4", "WarpPerRowSmem", "WarpPerRowSmemFp4");
+ * returns -1 for an unknown name.  The C++ parse_algorithm adds the
+ * reference's warn-and-fall-back-to-Naive behaviour on top
+ * (reference src/csrspmm.cpp:13-25). */
+int csrspmm_parse_algorithm(const char* name);
+
+/* Algorithm id -> CamelCase name, or NULL for an unknown id. */
+const char* csrspmm_algorithm_name(int algo);
+
+/* Bytes of device workspace csrspmm_spmm_f32_ws needs for this problem
+ * (row-split plan, partial sums of split rows, counters).  No counterpart in
+ * the reference, which has no long-row splitting. */
+size_t csrspmm_workspace_bytes(int algo, int M, int N, int nnz);
+
+/*
+ * The SpMM.  Replaces csrspmm::spmm's dispatch to launch_<variant>
+ * (reference src/csrspmm.cpp:28-71, src/host/spmm_launcher.cu:11-171) and the
+ * torch forwards' launch (reference torch_csrspmm/torch_csrspmm_*.cpp).
+ *   algo            CSRSPMM_ALGO_*
+ *   M, K, N, nnz    A is M x K with nnz nonzeros; B is K x N; C is M x N
+ *   rowptr, colidx, vals   device CSR arrays (M+1, nnz, nnz entries)
+ *   max_row_nnz_hint       -1 if unknown; otherwise the caller's claim of the
+ *                   longest row.  Used only to skip the row-split plan when
+ *                   every row is short; never used to size memory, so a
+ *                   wrong hint costs speed, not safety.
+ *   B, ldb, C, ldc  row-major dense operands, ldb >= N, ldc >= N
+ *   stream          hipStream_t (NULL = legacy default stream)
+ * Asynchronous: returns after enqueueing.  Uses a library-owned device
+ * workspace kept per (device, stream) and grown on demand; calls on one
+ * stream are ordered, calls on different streams use different workspaces.
+ */
+int csrspmm_spmm_f32(int algo, int M, int K, int N, int nnz,
+                     const int* rowptr, const int* colidx, const float* vals,
+                     int max_row_nnz_hint,
+                     const float* B, long long ldb,
+                     float* C, long long ldc,
+                     float alpha, float beta,
+                     void* stream);
+
+/* Flags for csrspmm_spmm_f32_ex. */
+enum {
+    /* Treat the prior contents of C as +0.0 without reading them:
+     * C = fma(alpha, sum, beta * 0.0f).  This is what the reference torch
+     * forwards compute by allocating C with zeros() whenever beta != 0
+     * (torch_csrspmm/torch_csrspmm_naive.cpp:32-34), without the memset and
+     * the read of C. */
+    CSRSPMM_FLAG_C_IS_ZERO = 1
+};
+
+/* As csrspmm_spmm_f32, with CSRSPMM_FLAG_* flags and a caller-provided
+ * device workspace of at least csrspmm_workspace_bytes(algo, M, N, nnz)
+ * bytes, 256-byte aligned (torch's caching allocator, for example; it may be
+ * NULL when that size is 0).  Allocates nothing.  The torch forwards call
+ * this entry point. */
+int csrspmm_spmm_f32_ex(int algo, int M, int K, int N, int nnz,
+                        const int* rowptr, const int* colidx, const float* vals,
+                        int max_row_nnz_hint,
+                        const float* B, long long ldb,
+                        float* C, long long ldc,
+                        float alpha, float beta,
+                        unsigned flags,
+                        void* workspace, size_t workspace_bytes,
+                        void* stream);
+
+/* Device-side CSR validation.  Writes the CSRSPMM_CSR_* bit set to
+ * *flags_out and the true longest row to *max_row_nnz_out (host pointers,
+ * either may be NULL); synchronises the stream.  Returns a status.  The
+ * reference has no validator; it stands in for the max_row_nnz scan that
+ * dense2csr performs on the host (reference src/host/csr_utils.cpp:106-110). */
+int csrspmm_validate_csr(int M, int K, int nnz,
+                         const int* rowptr, const int* colidx,
+                         int* flags_out, int* max_row_nnz_out,
+                         void* stream);
+
+/* Memory and device helpers that let the g++-built C++ layer stay free of
+ * HIP headers (they back csr_alloc_device / dense_alloc_device and the
+ * host<->device copies at reference src/host/csr_utils.cpp:44-67,183-238 and
+ * src/host/dense_utils.cpp:28-44,128-162). */
+int csrspmm_device_malloc(void** ptr, size_t bytes);
+int csrspmm_device_free(void* ptr);
+int csrspmm_memcpy_h2d(void* dst, const void* src, size_t bytes);
+int csrspmm_memcpy_d2h(void* dst, const void* src, size_t bytes);
+int csrspmm_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
+int csrspmm_device_synchronize(void);
+int csrspmm_stream_synchronize(void* stream);
+/* Returns and clears the last HIP error of this thread (cudaGetLastError at
+ * reference src/csrspmm.cpp:73). */
+int csrspmm_get_last_error(void);
+/* Number of visible devices (0 when no GPU); never initialises a context
+ * beyond what hipGetDeviceCount does. */
+int csrspmm_device_count(void);
+
+/* Kernel timing for benchmarks (no counterpart in the reference, whose bench
+ * times whole spmm() calls with cudaEvents, benchmarks/bench_csrspmm.cu:103-118).
+ * While enabled (process-wide), every SpMM call records a HIP event pair
+ * around its main kernel on the call's stream.  csrspmm_timing_read waits for
+ * the recorded pairs, returns the summed main-kernel milliseconds and the
+ * number of calls since the previous read, and recycles the events. */
+int csrspmm_timing_enable(int on);
+int csrspmm_timing_read(double* main_kernel_ms, int* calls);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CSRSPMM_C_H_ */
