@@ -20,33 +20,28 @@ static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 WorkspaceLayout workspace_layout(int M, int N, int nnz) {
   WorkspaceLayout L{};
-  const long long long_cap = std::min<long long>(M, (long long)nnz / (kSplitLen + 1));
-  const long long seg_cap = (long long)nnz / kSplitLen + 1 + long_cap;
-  L.long_cap = (int)long_cap;
-  L.seg_cap = (int)seg_cap;
+  L.nslots = nnz / kSplitLen;
+  L.nblocks = (int)(((long long)M + nnz + 1 + kMergeBlock - 1) / kMergeBlock);
   L.ldp = ((long long)N + 3) & ~3LL;
   size_t off = 0;
-  L.counters_off = off;
-  off = align256(off + 4 * sizeof(int));
+  L.block_start_off = off;
+  off = align256(off + ((size_t)L.nblocks + 1) * sizeof(int));
   L.seg_info_off = off;
-  off = align256(off + (size_t)seg_cap * sizeof(int2));
-  L.long_rows_off = off;
-  off = align256(off + (size_t)long_cap * sizeof(int4));
+  off = align256(off + (size_t)L.nslots * sizeof(int2));
   L.partials_off = off;
-  off = align256(off + (size_t)seg_cap * (size_t)L.ldp * sizeof(float));
+  off = align256(off + (size_t)L.nslots * (size_t)L.ldp * sizeof(float));
   L.total = off;
   return L;
 }
 
 void bind_workspace(Problem& p, void* ws, const WorkspaceLayout& L) {
   char* b = static_cast<char*>(ws);
-  p.counters = reinterpret_cast<int*>(b + L.counters_off);
+  p.block_start = reinterpret_cast<int*>(b + L.block_start_off);
   p.seg_info = reinterpret_cast<int2*>(b + L.seg_info_off);
-  p.long_rows = reinterpret_cast<int4*>(b + L.long_rows_off);
   p.partials = reinterpret_cast<float*>(b + L.partials_off);
   p.ldp = L.ldp;
-  p.seg_cap = L.seg_cap;
-  p.long_cap = L.long_cap;
+  p.nslots = L.nslots;
+  p.nblocks = L.nblocks;
 }
 
 namespace {
@@ -56,8 +51,12 @@ bool is_rowgroup(int algo) {
          algo == CSRSPMM_ALGO_WARP_PER_ROW_SMEM || algo == CSRSPMM_ALGO_WARP_PER_ROW_SMEM_FP4;
 }
 
-bool wants_plan(int algo, int hint) {
-  return is_rowgroup(algo) && (hint < 0 || hint > kSplitLen);
+// The plan pays for itself on large matrices (short rows are streamed,
+// long rows split); small ones with no long row run as one launch.
+bool wants_plan(int algo, int M, int nnz, int hint) {
+  if (!is_rowgroup(algo)) return false;
+  if ((long long)M + nnz >= kPlanMinItems) return true;
+  return (hint < 0 || hint > kSplitLen) && nnz > kSplitLen;
 }
 
 int to_status(hipError_t e) { return e == hipSuccess ? 0 : (int)e; }
@@ -108,8 +107,8 @@ int check_args(int algo, int M, int K, int N, int nnz, const int* rowptr, const 
   if (!rowptr || !C) return CSRSPMM_STATUS_INVALID_VALUE;
   if (nnz > 0 && (!colidx || !vals || !B || K == 0)) return CSRSPMM_STATUS_INVALID_VALUE;
   if (ldc < N || (nnz > 0 && ldb < N)) return CSRSPMM_STATUS_INVALID_VALUE;
-  // 64-bit offsets are used for B and C; the grid and row indices are 32-bit.
-  if ((long long)M * 64 > 0x7fffffffLL * 64LL) return CSRSPMM_STATUS_NOT_SUPPORTED;
+  // Merge coordinates (row + nonzero index) and grid sizes must fit int32.
+  if ((long long)M + nnz + 1 > 0x7fffffffLL - kMergeBlock) return CSRSPMM_STATUS_NOT_SUPPORTED;
   return 0;
 }
 
@@ -140,7 +139,7 @@ int spmm_impl(int algo, int M, int K, int N, int nnz, const int* rowptr, const i
     p.epi = kEpiZeroC;
   else
     p.epi = (beta == 0.0f) ? kEpiOverwrite : kEpiAccumulate;
-  p.plan = wants_plan(algo, hint) && nnz > kSplitLen;
+  p.plan = wants_plan(algo, M, nnz, hint);
 
   if (p.plan) {
     const WorkspaceLayout L = workspace_layout(M, N, nnz);
@@ -298,7 +297,7 @@ const char* csrspmm_algorithm_name(int algo) {
 }
 
 size_t csrspmm_workspace_bytes(int algo, int M, int N, int nnz) {
-  if (!is_rowgroup(algo) || M <= 0 || N <= 0 || nnz <= kSplitLen) return 0;
+  if (M <= 0 || N <= 0 || nnz < 0 || !wants_plan(algo, M, nnz, -1)) return 0;
   return workspace_layout(M, N, nnz).total;
 }
 

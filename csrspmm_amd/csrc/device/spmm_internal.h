@@ -18,14 +18,40 @@ enum EpilogueMode : int {
                        // it (the torch forwards' zeros()+beta, torch_csrspmm_naive.cpp:32-34)
 };
 
-// Segment length for splitting long rows.  A row longer than kSplitLen
-// nonzeros is cut into ceil(len / kSplitLen) segments of kSplitLen nonzeros
-// (the last one shorter); each segment's partial sum goes to the workspace
-// and a combine pass adds them in segment order.
-constexpr int kSplitLen = 256;
+// Long rows.  A row of len > kSplitLen nonzeros is cut into
+// floor(len / kSplitLen) segments: segment k covers nonzeros
+// [k*kSplitLen, (k+1)*kSplitLen) of the row and the last segment also takes
+// the remainder (so segments hold kSplitLen..2*kSplitLen-1 nonzeros).  Each
+// segment's partial sum goes to a workspace slot; a combine pass adds the
+// partials of a row in segment order and applies the epilogue.
+//
+// Slot ownership needs no counters: row r owns slots
+// [rowptr[r] / kSplitLen, rowptr[r+1] / kSplitLen), a range at least as long
+// as its segment count, and the ranges of all rows tile [0, nnz / kSplitLen).
+#ifndef CSRSPMM_SPLIT_LEN
+#define CSRSPMM_SPLIT_LEN 256
+#endif
+constexpr int kSplitLen = CSRSPMM_SPLIT_LEN;
+
+// Short rows (len <= kSplitLen) are streamed in merge-path blocks: with the
+// strictly increasing merge coordinate F(r) = r + rowptr[r], block b holds
+// the rows r with F(r) in [b*kMergeBlock, (b+1)*kMergeBlock), so every block
+// carries at most kMergeBlock (rows + nonzeros) of short-row work plus one
+// row's tail, and runs of empty rows are spread like nonzeros.
+#ifndef CSRSPMM_MERGE_BLOCK
+#define CSRSPMM_MERGE_BLOCK 128
+#endif
+constexpr int kMergeBlock = CSRSPMM_MERGE_BLOCK;
+
+// Below this many (rows + nonzeros) the plan is skipped and each row is
+// processed whole by one group (one launch instead of three).
+constexpr long long kPlanMinItems = 1 << 16;
 
 // Blocks of the persistent segment phase / combine phase: a few per CU.
-constexpr int kPersistentBlocks = 1024;
+#ifndef CSRSPMM_PERSISTENT_BLOCKS
+#define CSRSPMM_PERSISTENT_BLOCKS 1024
+#endif
+constexpr int kPersistentBlocks = CSRSPMM_PERSISTENT_BLOCKS;
 
 struct Problem {
   int M, K, N, nnz;
@@ -38,22 +64,21 @@ struct Problem {
   long long ldc;
   float alpha, beta;
   int epi;  // EpilogueMode
-  // Row-split plan (all inside the workspace); plan == false means every row
-  // is processed whole by its row group.
+  // Plan (all inside the workspace, all written by plan_kernel each call).
+  // plan == false: every row is processed whole by its own group.
   bool plan;
-  int* counters;     // [0] = #segments, [1] = #long rows, [2] = overflow flag
-  int2* seg_info;    // (row, segment index within row)
-  int4* long_rows;   // (row, first segment slot, #segments, 0)
-  float* partials;   // seg_cap x ldp floats
+  int nslots;         // nnz / kSplitLen
+  int nblocks;        // merge blocks
+  int* block_start;   // nblocks + 1 entries: first row of each merge block, then M
+  int2* seg_info;     // per slot: (row, segment index) or (-1, 0) for an unused slot
+  float* partials;    // nslots x ldp floats
   long long ldp;
-  int seg_cap;
-  int long_cap;
 };
 
 // Workspace layout for a problem (all offsets 256-byte aligned).
 struct WorkspaceLayout {
-  size_t counters_off, seg_info_off, long_rows_off, partials_off, total;
-  int seg_cap, long_cap;
+  size_t block_start_off, seg_info_off, partials_off, total;
+  int nslots, nblocks;
   long long ldp;
 };
 WorkspaceLayout workspace_layout(int M, int N, int nnz);
