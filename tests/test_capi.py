@@ -1,0 +1,111 @@
+"""The C ABI library loads on a machine without a GPU, exports every function
+include/*.h declares, and rejects bad arguments before touching the device."""
+import os
+import re
+
+import pytest
+
+from csrspmm_amd import ALGORITHMS, LIB_DIR, capi
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions(header):
+    text = open(os.path.join(ROOT, "include", header)).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(csrspmm_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.mark.parametrize("header,lib", [("csrspmm_c.h", "hip"), ("csrspmm_gen.h", "host")])
+def test_every_declared_symbol_is_exported(header, lib):
+    names = declared_functions(header)
+    assert len(names) >= 10
+    handle = capi.hip() if lib == "hip" else capi.host()
+    missing = [n for n in names if not hasattr(handle, n)]
+    assert not missing, missing
+    table = capi.HIP_API if lib == "hip" else capi.GEN_API
+    assert sorted(table) == names, "ctypes table out of sync with the header"
+
+
+def test_libraries_are_in_tree():
+    for name in ("libcsrspmm_hip.so", "libcsrspmm.so"):
+        assert os.path.exists(os.path.join(LIB_DIR, name))
+
+
+def test_parse_and_names():
+    lib = capi.hip()
+    for i, name in enumerate(ALGORITHMS):
+        assert lib.csrspmm_parse_algorithm(name.encode()) == i
+        assert lib.csrspmm_algorithm_name(i).decode() == name
+    assert lib.csrspmm_parse_algorithm(b"naive") == -1  # exact CamelCase match only
+    assert lib.csrspmm_parse_algorithm(b"Adaptive") == -1
+    assert lib.csrspmm_parse_algorithm(None) == -1
+    assert lib.csrspmm_algorithm_name(6) is None
+    assert lib.csrspmm_version() >= 100
+
+
+def test_status_strings():
+    lib = capi.hip()
+    for st in (0, -1, -2, -3, -4, -5, -99):
+        assert lib.csrspmm_status_string(st)
+    assert lib.csrspmm_status_string(-1).decode() == "invalid value"
+
+
+def _call(**kw):
+    args = dict(algo=3, M=4, K=4, N=4, nnz=0, rowptr=None, colidx=None, vals=None, hint=-1,
+                B=None, ldb=4, C=None, ldc=4, alpha=1.0, beta=0.0, stream=None)
+    args.update(kw)
+    return capi.hip().csrspmm_spmm_f32(args["algo"], args["M"], args["K"], args["N"], args["nnz"],
+                                       args["rowptr"], args["colidx"], args["vals"], args["hint"],
+                                       args["B"], args["ldb"], args["C"], args["ldc"],
+                                       args["alpha"], args["beta"], args["stream"])
+
+
+def test_argument_errors_without_device():
+    fake = 0x1000  # never dereferenced: every case fails validation first
+    assert _call(algo=-1) == -1
+    assert _call(algo=6) == -1
+    assert _call(M=-1) == -1
+    assert _call(nnz=-5) == -1
+    assert _call(rowptr=None, C=fake) == -1          # rowptr missing
+    assert _call(rowptr=fake, C=None) == -1          # C missing
+    assert _call(rowptr=fake, C=fake, nnz=3) == -1   # colidx / vals / B missing
+    assert _call(rowptr=fake, C=fake, ldc=3) == -1   # ldc < N
+    assert _call(rowptr=fake, C=fake, nnz=3, colidx=fake, vals=fake, B=fake, ldb=2) == -1
+    assert _call(rowptr=fake, C=fake, nnz=3, colidx=fake, vals=fake, B=fake, K=0) == -1
+    # merge coordinates beyond int32
+    assert _call(M=2**31 - 10, nnz=10, rowptr=fake, C=fake, colidx=fake, vals=fake, B=fake) == -2
+    # M == 0 or N == 0 is a successful no-op
+    assert _call(M=0) == 0
+    assert _call(N=0, ldc=0) == 0
+
+
+def test_workspace_bytes():
+    lib = capi.hip()
+    # Naive variants never need one; the warp family needs one for big problems.
+    assert lib.csrspmm_workspace_bytes(0, 100000, 128, 10**6) == 0
+    assert lib.csrspmm_workspace_bytes(1, 100000, 128, 10**6) == 0
+    big = lib.csrspmm_workspace_bytes(3, 262144, 128, 8453223)
+    nslots = 8453223 // 256
+    assert big >= nslots * 128 * 4 + nslots * 8 + (262144 + 8453223) // 128 * 4
+    assert big < 64 * 2**20
+    assert lib.csrspmm_workspace_bytes(3, 0, 128, 0) == 0
+    assert lib.csrspmm_workspace_bytes(3, 10, 16, 20) == 0  # tiny, no long row possible
+
+
+def test_ex_rejects_small_workspace_without_device():
+    lib = capi.hip()
+    fake = 0x1000
+    need = lib.csrspmm_workspace_bytes(3, 262144, 128, 8453223)
+    st = lib.csrspmm_spmm_f32_ex(3, 262144, 262144, 128, 8453223, fake, fake, fake, -1, fake, 128,
+                                 fake, 128, 1.0, 0.0, 0, fake, need - 1, None)
+    assert st == -5
+    st = lib.csrspmm_spmm_f32_ex(3, 262144, 262144, 128, 8453223, fake, fake, fake, -1, fake, 128,
+                                 fake, 128, 1.0, 0.0, 0, fake + 8, need, None)
+    assert st == -1  # misaligned workspace
+
+
+def test_validate_rejects_bad_sizes_without_device():
+    lib = capi.hip()
+    assert lib.csrspmm_validate_csr(-1, 4, 0, None, None, None, None, None) == -1
+    assert lib.csrspmm_validate_csr(4, 4, 0, None, None, None, None, None) == -1

@@ -1,0 +1,45 @@
+"""The torch_csrspmm drop-in imports on a CPU-only machine, exposes the
+reference's five entry points with the reference's argument lists
+(torch_csrspmm/__init__.py:10-23), and raises the reference's RuntimeError for
+host tensors (torch_csrspmm/torch_csrspmm_naive.cpp:22-25)."""
+import inspect
+
+import pytest
+import torch
+
+import csrspmm_amd.torch_csrspmm as tc
+
+SIGS = {
+    "csrspmm_naive": ["A_rowptr", "A_colidx", "A_values", "B", "alpha", "beta"],
+    "csrspmm_warp_per_row": ["A_rowptr", "A_colidx", "A_values", "B", "alpha", "beta"],
+    "csrspmm_warp_per_row_fp4": ["A_rowptr", "A_colidx", "A_values", "B", "alpha", "beta"],
+    "csrspmm_warp_per_row_smem": ["A_rowptr", "A_colidx", "A_values", "A_max_row_nnz", "B",
+                                  "alpha", "beta"],
+    "csrspmm_warp_per_row_smem_fp4": ["A_rowptr", "A_colidx", "A_values", "A_max_row_nnz", "B",
+                                      "alpha", "beta"],
+}
+
+
+def test_entry_points_and_signatures():
+    assert sorted(tc.__all__) == sorted(SIGS)
+    for name, params in SIGS.items():
+        assert list(inspect.signature(getattr(tc, name)).parameters) == params
+        assert hasattr(tc._C, name)
+    assert tc._C.__file__.startswith(tc.__file__.rsplit("/", 1)[0])  # in-tree extension
+
+
+def cpu_inputs():
+    rowptr = torch.tensor([0, 1, 2], dtype=torch.int32)
+    colidx = torch.tensor([0, 1], dtype=torch.int32)
+    vals = torch.ones(2)
+    B = torch.ones(2, 4)
+    return rowptr, colidx, vals, B
+
+
+@pytest.mark.parametrize("name", sorted(SIGS))
+def test_host_tensors_raise(name):
+    rowptr, colidx, vals, B = cpu_inputs()
+    fn = getattr(tc, name)
+    args = (rowptr, colidx, vals, 1, B, 1.0, 0.0) if "smem" in name else (rowptr, colidx, vals, B, 1.0, 0.0)
+    with pytest.raises(RuntimeError, match="A_row_ptr must be a CUDA tensor"):
+        fn(*args)
