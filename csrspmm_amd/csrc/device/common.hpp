@@ -24,10 +24,24 @@ template <> struct Vec<4> {
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
 
+// Cache policy knobs (build-time): non-temporal A loads and C stores.
+#ifndef CSRSPMM_NT_A
+#define CSRSPMM_NT_A 1
+#endif
+#ifndef CSRSPMM_NT_C
+#define CSRSPMM_NT_C 1
+#endif
+
 // A (colidx, values) is streamed exactly once: load it non-temporally so it
 // does not push gathered B rows out of L2 / the MALL.
-__device__ __forceinline__ int ld_stream(const int* p) { return __builtin_nontemporal_load(p); }
-__device__ __forceinline__ float ld_stream(const float* p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ int ld_stream(const int* p) {
+  if constexpr (CSRSPMM_NT_A) return __builtin_nontemporal_load(p);
+  return *p;
+}
+__device__ __forceinline__ float ld_stream(const float* p) {
+  if constexpr (CSRSPMM_NT_A) return __builtin_nontemporal_load(p);
+  return *p;
+}
 
 // B rows are gathered (reused across rows that share a column): normal cached loads.
 template <int VEC>
@@ -36,9 +50,19 @@ __device__ __forceinline__ typename Vec<VEC>::T ld_b(const float* p) {
 }
 
 // C is written once: non-temporal stores keep it out of the caches B lives in.
-__device__ __forceinline__ void st_c(float* p, float v) { __builtin_nontemporal_store(v, p); }
+__device__ __forceinline__ void st_c(float* p, float v) {
+  if constexpr (CSRSPMM_NT_C) {
+    __builtin_nontemporal_store(v, p);
+  } else {
+    *p = v;
+  }
+}
 __device__ __forceinline__ void st_c(float* p, f4 v) {
-  __builtin_nontemporal_store(v, reinterpret_cast<f4*>(p));
+  if constexpr (CSRSPMM_NT_C) {
+    __builtin_nontemporal_store(v, reinterpret_cast<f4*>(p));
+  } else {
+    *reinterpret_cast<f4*>(p) = v;
+  }
 }
 
 __device__ __forceinline__ float fmaf_(float a, float b, float c) { return __builtin_fmaf(a, b, c); }

@@ -302,11 +302,17 @@ __global__ __launch_bounds__(256) void plan_kernel(Problem p) {
 }
 
 // One wave per long row (found at its first slot): C[row] = epilogue(sum of
-// the row's segment partials in segment order).
-template <int VEC>
+// the row's segment partials).  The wave is split into P = 64 / GC lane
+// groups (GC lanes cover a column panel); group q sums segments q, q+P, ...
+// in order, then the P group sums are added by a fixed xor-shuffle tree, so
+// the result does not depend on timing.
+template <int VEC, int GC>
 __global__ __launch_bounds__(256) void combine_kernel(Problem p) {
   using VT = typename Vec<VEC>::T;
+  constexpr int P = 64 / GC;
   const int lane = lane_id();
+  const int q = lane / GC;
+  const int gl = lane & (GC - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nw = blockDim.x >> 6;
   for (int s = blockIdx.x * nw + wave; s < p.nslots; s += gridDim.x * nw) {
@@ -314,20 +320,49 @@ __global__ __launch_bounds__(256) void combine_kernel(Problem p) {
     if (si.x < 0 || si.x >= p.M || si.y != 0) continue;
     const int nseg = (p.rowptr[si.x + 1] - p.rowptr[si.x]) / kSplitLen;
     float* crow = p.C + (long long)si.x * p.ldc;
-    for (int c = lane * VEC; c < p.N; c += 64 * VEC) {
+    for (int c0 = 0; c0 < p.N; c0 += GC * VEC) {
+      const int c = c0 + gl * VEC;
+      const bool cv = c < p.N;
       const float* src = p.partials + (long long)s * p.ldp + c;
       VT acc = Vec<VEC>::zero();
-      int k = 0;
-      for (; k + 4 <= nseg; k += 4) {
-        const VT a0 = *reinterpret_cast<const VT*>(src + (long long)(k + 0) * p.ldp);
-        const VT a1 = *reinterpret_cast<const VT*>(src + (long long)(k + 1) * p.ldp);
-        const VT a2 = *reinterpret_cast<const VT*>(src + (long long)(k + 2) * p.ldp);
-        const VT a3 = *reinterpret_cast<const VT*>(src + (long long)(k + 3) * p.ldp);
-        acc = add_v(add_v(add_v(add_v(acc, a0), a1), a2), a3);
+      int k = q;
+      for (; k + 3 * P < nseg; k += 4 * P) {
+        VT a[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          a[u] = cv ? *reinterpret_cast<const VT*>(src + (long long)(k + u * P) * p.ldp) : Vec<VEC>::zero();
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc = add_v(acc, a[u]);
       }
-      for (; k < nseg; ++k) acc = add_v(acc, *reinterpret_cast<const VT*>(src + (long long)k * p.ldp));
-      store_epi<VEC>(p, crow + c, acc);
+      for (; k < nseg; k += P)
+        if (cv) acc = add_v(acc, *reinterpret_cast<const VT*>(src + (long long)k * p.ldp));
+#pragma unroll
+      for (int off = GC; off < 64; off <<= 1) {
+        if constexpr (VEC == 1) {
+          acc += __shfl_xor(acc, off);
+        } else {
+          acc.x += __shfl_xor(acc.x, off);
+          acc.y += __shfl_xor(acc.y, off);
+          acc.z += __shfl_xor(acc.z, off);
+          acc.w += __shfl_xor(acc.w, off);
+        }
+      }
+      if (q == 0 && cv) store_epi<VEC>(p, crow + c, acc);
     }
+  }
+}
+
+template <int VEC>
+void launch_combine(const Problem& p, int blocks, hipStream_t s) {
+  const int chunks = (p.N + VEC - 1) / VEC;
+  if (chunks <= 8) {
+    hipLaunchKernelGGL((combine_kernel<VEC, 8>), dim3(blocks), dim3(256), 0, s, p);
+  } else if (chunks <= 16) {
+    hipLaunchKernelGGL((combine_kernel<VEC, 16>), dim3(blocks), dim3(256), 0, s, p);
+  } else if (chunks <= 32) {
+    hipLaunchKernelGGL((combine_kernel<VEC, 32>), dim3(blocks), dim3(256), 0, s, p);
+  } else {
+    hipLaunchKernelGGL((combine_kernel<VEC, 64>), dim3(blocks), dim3(256), 0, s, p);
   }
 }
 
@@ -407,11 +442,11 @@ hipError_t launch_rowgroup(const Problem& p, int vec, bool lds, hipStream_t s) {
   }
   if (e != hipSuccess) return e;
   if (p.plan && p.nslots > 0) {
-    const int cblocks = std::min(kPersistentBlocks / 2, div_up_host(p.nslots, 4));
+    const int cblocks = std::min(kPersistentBlocks, div_up_host(p.nslots, 4));
     if (vec == 4) {
-      hipLaunchKernelGGL(combine_kernel<4>, dim3(cblocks), dim3(256), 0, s, p);
+      launch_combine<4>(p, cblocks, s);
     } else {
-      hipLaunchKernelGGL(combine_kernel<1>, dim3(cblocks), dim3(256), 0, s, p);
+      launch_combine<1>(p, cblocks, s);
     }
     e = hipGetLastError();
   }
