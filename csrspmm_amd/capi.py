@@ -18,7 +18,7 @@ _c_int, _c_ll, _c_float, _c_void_p, _c_size_t = (ctypes.c_int, ctypes.c_longlong
 _c_u64 = ctypes.c_uint64
 
 ALGO = {"Naive": 0, "NaiveSmem": 1, "WarpPerRow": 2, "WarpPerRowFp4": 3, "WarpPerRowSmem": 4,
-        "WarpPerRowSmemFp4": 5}
+        "WarpPerRowSmemFp4": 5, "Auto": 6}
 FLAG_C_IS_ZERO = 1
 
 # Every function include/csrspmm_c.h declares: name -> (restype, argtypes).
@@ -27,6 +27,7 @@ HIP_API = {
     "csrspmm_status_string": (ctypes.c_char_p, [_c_int]),
     "csrspmm_parse_algorithm": (_c_int, [ctypes.c_char_p]),
     "csrspmm_algorithm_name": (ctypes.c_char_p, [_c_int]),
+    "csrspmm_resolve_algorithm": (_c_int, [_c_int, _c_int]),
     "csrspmm_workspace_bytes": (_c_size_t, [_c_int, _c_int, _c_int, _c_int]),
     "csrspmm_spmm_f32": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p, _c_void_p,
                                   _c_void_p, _c_int, _c_void_p, _c_ll, _c_void_p, _c_ll, _c_float,
@@ -35,6 +36,14 @@ HIP_API = {
                                      _c_void_p, _c_int, _c_void_p, _c_ll, _c_void_p, _c_ll,
                                      _c_float, _c_float, ctypes.c_uint, _c_void_p, _c_size_t,
                                      _c_void_p]),
+    "csrspmm_plan_create": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_void_p, _c_void_p, _c_void_p,
+                                     _c_int, _c_void_p, ctypes.POINTER(_c_void_p)]),
+    "csrspmm_plan_spmm_f32": (_c_int, [_c_void_p, _c_int, _c_void_p, _c_ll, _c_void_p, _c_ll, _c_float,
+                                       _c_float, ctypes.c_uint, _c_void_p]),
+    "csrspmm_plan_algorithm": (_c_int, [_c_void_p]),
+    "csrspmm_plan_device_bytes": (_c_size_t, [_c_void_p]),
+    "csrspmm_plan_panelized_rows": (_c_int, [_c_void_p]),
+    "csrspmm_plan_destroy": (_c_int, [_c_void_p]),
     "csrspmm_validate_csr": (_c_int, [_c_int, _c_int, _c_int, _c_void_p, _c_void_p,
                                       ctypes.POINTER(_c_int), ctypes.POINTER(_c_int), _c_void_p]),
     "csrspmm_device_malloc": (_c_int, [ctypes.POINTER(_c_void_p), _c_size_t]),
@@ -148,6 +157,57 @@ def spmm(algo, rowptr, colidx, vals, B, C, alpha, beta, *, M=None, K=None, hint=
                                      _ptr(workspace), wsz, ctypes.c_void_p(stream))
     check(st, f"csrspmm_spmm {algo}")
     return C
+
+
+class Plan:
+    """A stored plan (csrspmm_plan_*) for one CSR matrix on the GPU.  Keeps
+    references to the CSR tensors, which the plan uses in place."""
+
+    def __init__(self, algo, rowptr, colidx, vals, K, n_hint=-1, stream=None):
+        a = ALGO[algo] if isinstance(algo, str) else int(algo)
+        self._keep = (rowptr, colidx, vals)
+        self.M = rowptr.numel() - 1
+        self.K = K
+        if stream is None:
+            stream = torch.cuda.current_stream(rowptr.device).cuda_stream
+        h = _c_void_p()
+        check(hip().csrspmm_plan_create(a, self.M, K, vals.numel(), _ptr(rowptr), _ptr(colidx),
+                                        _ptr(vals), n_hint, ctypes.c_void_p(stream),
+                                        ctypes.byref(h)), "csrspmm_plan_create")
+        self._h = h
+
+    @property
+    def algorithm(self) -> str:
+        return hip().csrspmm_algorithm_name(hip().csrspmm_plan_algorithm(self._h)).decode()
+
+    @property
+    def device_bytes(self) -> int:
+        return hip().csrspmm_plan_device_bytes(self._h)
+
+    @property
+    def panelized_rows(self) -> int:
+        return hip().csrspmm_plan_panelized_rows(self._h)
+
+    def spmm(self, B, C, alpha, beta, flags=0, stream=None):
+        if stream is None:
+            stream = torch.cuda.current_stream(C.device).cuda_stream
+        N = C.shape[1]
+        ldb = B.stride(0) if B.shape[1] > 1 else max(N, 1)
+        ldc = C.stride(0) if N > 1 else max(N, 1)
+        check(hip().csrspmm_plan_spmm_f32(self._h, N, _ptr(B), ldb, _ptr(C), ldc, alpha, beta, flags,
+                                          ctypes.c_void_p(stream)), "csrspmm_plan_spmm_f32")
+        return C
+
+    def close(self):
+        if self._h:
+            check(hip().csrspmm_plan_destroy(self._h), "csrspmm_plan_destroy")
+            self._h = _c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def timing_enable(on: bool) -> None:

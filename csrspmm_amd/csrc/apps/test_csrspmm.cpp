@@ -30,7 +30,7 @@ int main(int argc, char** argv) {
             std::cout << "Usage: " << argv[0]
                       << " [-M rows] [-N cols of A] [-K cols of B] [-s sparsity] [-a alpha] [-b beta]"
                          " [-algo Naive|NaiveSmem|WarpPerRow|WarpPerRowFp4|WarpPerRowSmem|"
-                         "WarpPerRowSmemFp4|all]\n";
+                         "WarpPerRowSmemFp4|Auto|all]\n";
             return 0;
         } else {
             std::cerr << "Unknown or incomplete flag: " << arg << std::endl;
@@ -39,7 +39,8 @@ int main(int argc, char** argv) {
     }
     std::vector<std::string> algos;
     if (algo_str == "all")
-        algos = {"Naive", "NaiveSmem", "WarpPerRow", "WarpPerRowFp4", "WarpPerRowSmem", "WarpPerRowSmemFp4"};
+        algos = {"Naive", "NaiveSmem", "WarpPerRow", "WarpPerRowFp4", "WarpPerRowSmem", "WarpPerRowSmemFp4",
+                 "Auto"};
     else
         algos = {algo_str};
 
@@ -74,6 +75,18 @@ int main(int argc, char** argv) {
         std::cout << (ok ? "Pass: " : "Error: ") << name << " M=" << M << " N=" << N << " K=" << K
                   << " nnz=" << hA_csr.nnz << std::endl;
         failures += ok ? 0 : 1;
+        // the same product through a stored plan, twice
+        {
+            csrspmm::dense_free_device(dC);
+            csrspmm::dense_host2device(hC, dC);
+            csrspmm::SpmmPlan plan(dA, algo, K);
+            plan.run(dB, dC, alpha, beta);
+            csrspmm::dense_free_host(hOut);
+            csrspmm::dense_device2host(dC, hOut);
+            const bool ok2 = csrspmm::dense_compare(hOut, hRef, 1e-2f);
+            std::cout << (ok2 ? "Pass: " : "Error: ") << name << " (plan)" << std::endl;
+            failures += ok2 ? 0 : 1;
+        }
         csrspmm::dense_free_host(hOut);
         csrspmm::csr_free_device(dA);
         csrspmm::dense_free_device(dB);

@@ -99,33 +99,52 @@ int owned_workspace(void* stream, size_t bytes, void** out) {
   return 0;
 }
 
-int check_args(int algo, int M, int K, int N, int nnz, const int* rowptr, const int* colidx,
-               const float* vals, const float* B, long long ldb, const float* C, long long ldc) {
+}  // namespace
+
+int resolve_algorithm(int algo, int N) {
+  if (algo == CSRSPMM_ALGO_AUTO) {
+    // Measured on MI355X: the LDS-staged warp-per-row forms lead on every
+    // config; float4 columns win from N = 128 up, scalar columns below
+    // (64-lane groups instead of 16-lane float4 groups).
+    return (N % 4 == 0 && N >= 128) ? CSRSPMM_ALGO_WARP_PER_ROW_SMEM_FP4 : CSRSPMM_ALGO_WARP_PER_ROW_SMEM;
+  }
+  if (algo < 0 || algo >= CSRSPMM_ALGO_COUNT) return -1;
+  return algo;
+}
+
+bool is_rowgroup_algorithm(int algo) { return is_rowgroup(algo); }
+
+bool uses_lds(int algo) {
+  return algo == CSRSPMM_ALGO_WARP_PER_ROW_SMEM || algo == CSRSPMM_ALGO_WARP_PER_ROW_SMEM_FP4;
+}
+
+int vector_width(int algo, const Problem& p) {
+  if (algo != CSRSPMM_ALGO_WARP_PER_ROW_FP4 && algo != CSRSPMM_ALGO_WARP_PER_ROW_SMEM_FP4) return 1;
+  // The float4 forms need 16-byte aligned rows of B and C; otherwise the
+  // scalar-column kernel of the same family runs (the reference instead drops
+  // the last N % 4 columns, csrspmm_warp_per_row_fp4.cu:29-32).
+  const bool ok = (p.N % 4 == 0) && (p.ldc % 4 == 0) &&
+                  ((reinterpret_cast<uintptr_t>(p.C) & 15) == 0) &&
+                  (p.nnz == 0 || ((p.ldb % 4 == 0) && ((reinterpret_cast<uintptr_t>(p.B) & 15) == 0)));
+  return ok ? 4 : 1;
+}
+
+int fill_problem(Problem& p, int algo, int M, int K, int N, int nnz, const int* rowptr,
+                 const int* colidx, const float* vals, const float* B, long long ldb, float* C,
+                 long long ldc, float alpha, float beta, unsigned flags) {
   if (algo < 0 || algo >= CSRSPMM_ALGO_COUNT) return CSRSPMM_STATUS_INVALID_VALUE;
   if (M < 0 || K < 0 || N < 0 || nnz < 0) return CSRSPMM_STATUS_INVALID_VALUE;
+  p = Problem{};
+  p.M = M;
+  p.K = K;
+  p.N = N;
+  p.nnz = nnz;
   if (M == 0 || N == 0) return 0;
   if (!rowptr || !C) return CSRSPMM_STATUS_INVALID_VALUE;
   if (nnz > 0 && (!colidx || !vals || !B || K == 0)) return CSRSPMM_STATUS_INVALID_VALUE;
   if (ldc < N || (nnz > 0 && ldb < N)) return CSRSPMM_STATUS_INVALID_VALUE;
   // Merge coordinates (row + nonzero index) and grid sizes must fit int32.
   if ((long long)M + nnz + 1 > 0x7fffffffLL - kMergeBlock) return CSRSPMM_STATUS_NOT_SUPPORTED;
-  return 0;
-}
-
-int spmm_impl(int algo, int M, int K, int N, int nnz, const int* rowptr, const int* colidx,
-              const float* vals, int hint, const float* B, long long ldb, float* C, long long ldc,
-              float alpha, float beta, unsigned flags, void* ws, size_t ws_bytes, bool owned,
-              void* stream) {
-  int st = check_args(algo, M, K, N, nnz, rowptr, colidx, vals, B, ldb, C, ldc);
-  if (st != 0) return st;
-  if (M == 0 || N == 0) return 0;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-
-  Problem p{};
-  p.M = M;
-  p.K = K;
-  p.N = N;
-  p.nnz = nnz;
   p.rowptr = rowptr;
   p.colidx = colidx;
   p.vals = vals;
@@ -135,12 +154,39 @@ int spmm_impl(int algo, int M, int K, int N, int nnz, const int* rowptr, const i
   p.ldc = ldc;
   p.alpha = alpha;
   p.beta = beta;
-  if (flags & 1u)
+  if (flags & CSRSPMM_FLAG_C_IS_ZERO)
     p.epi = kEpiZeroC;
   else
     p.epi = (beta == 0.0f) ? kEpiOverwrite : kEpiAccumulate;
-  p.plan = wants_plan(algo, M, nnz, hint);
+  return 0;
+}
 
+hipError_t launch_algorithm(int algo, const Problem& p, hipStream_t s) {
+  const int vec = vector_width(algo, p);
+  switch (algo) {
+    case CSRSPMM_ALGO_NAIVE: return launch_naive(p, s);
+    case CSRSPMM_ALGO_NAIVE_SMEM: return launch_naive_smem(p, s);
+    case CSRSPMM_ALGO_WARP_PER_ROW:
+    case CSRSPMM_ALGO_WARP_PER_ROW_FP4:
+    case CSRSPMM_ALGO_WARP_PER_ROW_SMEM:
+    case CSRSPMM_ALGO_WARP_PER_ROW_SMEM_FP4: return launch_rowgroup(p, vec, uses_lds(algo), s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+namespace {
+
+int spmm_impl(int algo_in, int M, int K, int N, int nnz, const int* rowptr, const int* colidx,
+              const float* vals, int hint, const float* B, long long ldb, float* C, long long ldc,
+              float alpha, float beta, unsigned flags, void* ws, size_t ws_bytes, bool owned,
+              void* stream) {
+  const int algo = resolve_algorithm(algo_in, N);
+  Problem p;
+  int st = fill_problem(p, algo, M, K, N, nnz, rowptr, colidx, vals, B, ldb, C, ldc, alpha, beta, flags);
+  if (st != 0) return st;
+  if (M == 0 || N == 0) return 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  p.plan = wants_plan(algo, M, nnz, hint);
   if (p.plan) {
     const WorkspaceLayout L = workspace_layout(M, N, nnz);
     if (owned) {
@@ -152,24 +198,7 @@ int spmm_impl(int algo, int M, int K, int N, int nnz, const int* rowptr, const i
     }
     bind_workspace(p, ws, L);
   }
-
-  // The float4 forms need 16-byte aligned rows of B and C; otherwise the
-  // scalar-column kernel of the same family runs (the reference instead drops
-  // the last N % 4 columns, csrspmm_warp_per_row_fp4.cu:29-32).
-  const bool vec_ok = (N % 4 == 0) && (ldc % 4 == 0) &&
-                      ((reinterpret_cast<uintptr_t>(C) & 15) == 0) &&
-                      (nnz == 0 || ((ldb % 4 == 0) && ((reinterpret_cast<uintptr_t>(B) & 15) == 0)));
-  hipError_t e = hipSuccess;
-  switch (algo) {
-    case CSRSPMM_ALGO_NAIVE: e = launch_naive(p, s); break;
-    case CSRSPMM_ALGO_NAIVE_SMEM: e = launch_naive_smem(p, s); break;
-    case CSRSPMM_ALGO_WARP_PER_ROW: e = launch_rowgroup(p, 1, false, s); break;
-    case CSRSPMM_ALGO_WARP_PER_ROW_FP4: e = launch_rowgroup(p, vec_ok ? 4 : 1, false, s); break;
-    case CSRSPMM_ALGO_WARP_PER_ROW_SMEM: e = launch_rowgroup(p, 1, true, s); break;
-    case CSRSPMM_ALGO_WARP_PER_ROW_SMEM_FP4: e = launch_rowgroup(p, vec_ok ? 4 : 1, true, s); break;
-    default: return CSRSPMM_STATUS_INVALID_VALUE;
-  }
-  return to_status(e);
+  return to_status(launch_algorithm(algo, p, s));
 }
 
 // One wave per row: rowptr monotonicity and row length (lane 0), column
@@ -227,7 +256,10 @@ size_t g_t_used = 0;
 
 }  // namespace
 
+thread_local int t_timing_depth = 0;
+
 void timing_before_main(hipStream_t s) {
+  if (t_timing_depth++ > 0) return;
   std::lock_guard<std::mutex> lock(g_t_mutex);
   if (!g_t_on) return;
   if (g_t_used == g_t_events.size()) {
@@ -243,6 +275,7 @@ void timing_before_main(hipStream_t s) {
 }
 
 void timing_after_main(hipStream_t s) {
+  if (--t_timing_depth > 0) return;
   std::lock_guard<std::mutex> lock(g_t_mutex);
   if (!g_t_on || g_t_used == g_t_events.size()) return;
   (void)hipEventRecord(g_t_events[g_t_used].second, s);
@@ -281,22 +314,26 @@ const char* csrspmm_status_string(int status) {
   }
 }
 
-static const char* const kAlgoNames[CSRSPMM_ALGO_COUNT] = {
-    "Naive", "NaiveSmem", "WarpPerRow", "WarpPerRowFp4", "WarpPerRowSmem", "WarpPerRowSmemFp4"};
+static const char* const kAlgoNames[CSRSPMM_ALGO_COUNT + 1] = {
+    "Naive", "NaiveSmem", "WarpPerRow", "WarpPerRowFp4", "WarpPerRowSmem", "WarpPerRowSmemFp4",
+    "Auto"};
 
 int csrspmm_parse_algorithm(const char* name) {
   if (!name) return -1;
-  for (int i = 0; i < CSRSPMM_ALGO_COUNT; ++i)
+  for (int i = 0; i <= CSRSPMM_ALGO_COUNT; ++i)
     if (strcmp(name, kAlgoNames[i]) == 0) return i;
   return -1;
 }
 
 const char* csrspmm_algorithm_name(int algo) {
-  if (algo < 0 || algo >= CSRSPMM_ALGO_COUNT) return nullptr;
+  if (algo < 0 || algo > CSRSPMM_ALGO_COUNT) return nullptr;
   return kAlgoNames[algo];
 }
 
+int csrspmm_resolve_algorithm(int algo, int N) { return resolve_algorithm(algo, N); }
+
 size_t csrspmm_workspace_bytes(int algo, int M, int N, int nnz) {
+  algo = resolve_algorithm(algo, N);
   if (M <= 0 || N <= 0 || nnz < 0 || !wants_plan(algo, M, nnz, -1)) return 0;
   return workspace_layout(M, N, nnz).total;
 }

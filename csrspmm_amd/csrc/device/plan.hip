@@ -1,0 +1,443 @@
+// Stored SpMM plans (csrspmm_plan_* in include/csrspmm_c.h).
+//
+// A plan analyses A once: it picks the variant (CSRSPMM_ALGO_AUTO), builds
+// the merge-block starts and long-row segment slots that plan_kernel would
+// otherwise rebuild on every call, and "panelizes" very long rows on a large
+// B.  That last step is what a per-call path cannot afford.
+//
+// Panelized rows.  A row of at least kPanelMinLen nonzeros with sorted
+// columns is cut at column-panel boundaries (P panels of K/P columns, the
+// B band of a panel is ~kPanelBandBytes) into pieces of at most kSplitLen
+// nonzeros.  Panels are dealt to the 8 XCDs in column order, each to the
+// least-loaded XCD; the pieces of an XCD's panels, in panel order, form its
+// list, and each list is cut into units of ~kPanelUnitItems
+// (nonzeros + pieces), and the units are laid out in chunks of one
+// workgroup's worth (GPB units) taking the XCD lists in turn.  Chunk c is
+// workgroup c, which the hardware dispatches to XCD c mod 8, so every XCD
+// works through its own panels in order and the B rows it gathers at any
+// time fit in its L2.  The pieces are copied into a derived CSR (one row per
+// piece, rows in unit order) and streamed by the ordinary short-row kernel
+// into a partial buffer; the combine pass adds a row's pieces in column
+// order.  Measured on the XL config, in isolation, this cut the long-row
+// part from 562 us to 352 us.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "../../../include/csrspmm_c.h"
+#include "common.hpp"
+#include "spmm_internal.h"
+
+#ifndef CSRSPMM_PANEL_MIN_LEN
+#define CSRSPMM_PANEL_MIN_LEN 2048
+#endif
+#ifndef CSRSPMM_PANEL_BAND_KB
+#define CSRSPMM_PANEL_BAND_KB 512
+#endif
+#ifndef CSRSPMM_PANEL_UNIT_ITEMS
+#define CSRSPMM_PANEL_UNIT_ITEMS 64
+#endif
+
+namespace csrspmm_hip {
+namespace {
+
+constexpr int kPanelMinLen = CSRSPMM_PANEL_MIN_LEN;
+constexpr long long kPanelBandBytes = (long long)CSRSPMM_PANEL_BAND_KB * 1024;
+constexpr int kPanelUnitItems = CSRSPMM_PANEL_UNIT_ITEMS;
+constexpr int kPanelMaxPanels = 256;
+constexpr int kPanelSkewMax = 4;  // max panel load over mean panel load
+
+// Panels for a K x N fp32 B: a power of two (>= kXcds) giving a band of about
+// kPanelBandBytes; 0 (off) when B is small enough for the L2s, N is wide, or
+// the band knob is 0.
+int panel_count(int K, int N) {
+  const long long bbytes = (long long)K * N * 4;
+  if (kPanelBandBytes <= 0 || N > 256 || bbytes < 16LL * 1024 * 1024) return 0;
+  long long p = kXcds;
+  while (p * 2 <= kPanelMaxPanels && p * 2 * kPanelBandBytes <= bbytes) p *= 2;
+  return (int)p;
+}
+
+// Groups (rows) per workgroup of the kernel launch_rowgroup picks for N.
+int groups_per_block(int vec, int N) {
+  const int chunks = vec == 4 ? N / 4 : N;
+  int g = 4;
+  while (g < chunks && g < 64) g <<= 1;
+  return 4 * (64 / g);
+}
+
+struct Dev {
+  std::vector<void*> ptrs;
+  size_t bytes = 0;
+  template <class T>
+  hipError_t alloc_copy(T** out, const std::vector<T>& host) {
+    *out = nullptr;
+    if (host.empty()) return hipSuccess;
+    const size_t b = host.size() * sizeof(T);
+    hipError_t e = hipMalloc(reinterpret_cast<void**>(out), b);
+    if (e != hipSuccess) return e;
+    ptrs.push_back(*out);
+    bytes += b;
+    return hipMemcpy(*out, host.data(), b, hipMemcpyHostToDevice);
+  }
+};
+
+}  // namespace
+}  // namespace csrspmm_hip
+
+using namespace csrspmm_hip;
+
+struct csrspmm_plan_s {
+  int algo = 0;
+  int M = 0, K = 0, nnz = 0;
+  const int* rowptr = nullptr;
+  const int* colidx = nullptr;
+  const float* vals = nullptr;
+  bool use_plan = false;
+  int maxlen = 0;
+  int nslots = 0, nblocks = 0;
+  int* d_block_start = nullptr;
+  int2* d_seg_info = nullptr;
+  // panelized rows
+  int npan = 0, npieces = 0, nunits = 0;
+  int* d_pan_rows = nullptr;
+  int* d_pan_ptr = nullptr;
+  int* d_pan_piece = nullptr;
+  int* d_drowptr = nullptr;
+  int* d_dcolidx = nullptr;
+  float* d_dvals = nullptr;
+  int* d_unit_start = nullptr;
+  // partial buffers, grown with N
+  long long ldp_cap = 0;
+  float* d_partials = nullptr;
+  float* d_pan_part = nullptr;
+  Dev dev;
+  size_t partial_bytes = 0;
+};
+
+namespace {
+
+void plan_free(csrspmm_plan_s* p) {
+  for (void* q : p->dev.ptrs) (void)hipFree(q);
+  if (p->d_partials) (void)hipFree(p->d_partials);
+  if (p->d_pan_part) (void)hipFree(p->d_pan_part);
+  delete p;
+}
+
+hipError_t ensure_partials(csrspmm_plan_s* p, int N, hipStream_t s) {
+  const long long ldp = ((long long)N + 3) & ~3LL;
+  if (ldp <= p->ldp_cap) return hipSuccess;
+  hipError_t e = hipStreamSynchronize(s);  // earlier calls may still read the old buffers
+  if (e != hipSuccess) return e;
+  if (p->d_partials) (void)hipFree(p->d_partials);
+  if (p->d_pan_part) (void)hipFree(p->d_pan_part);
+  p->d_partials = p->d_pan_part = nullptr;
+  p->ldp_cap = 0;
+  p->partial_bytes = 0;
+  if (p->nslots > 0) {
+    e = hipMalloc(reinterpret_cast<void**>(&p->d_partials), (size_t)p->nslots * ldp * sizeof(float));
+    if (e != hipSuccess) return e;
+  }
+  if (p->npieces > 0) {
+    e = hipMalloc(reinterpret_cast<void**>(&p->d_pan_part), (size_t)p->npieces * ldp * sizeof(float));
+    if (e != hipSuccess) return e;
+  }
+  p->ldp_cap = ldp;
+  p->partial_bytes = ((size_t)p->nslots + (size_t)p->npieces) * ldp * sizeof(float);
+  return hipSuccess;
+}
+
+int to_status(hipError_t e) { return e == hipSuccess ? 0 : (int)e; }
+
+// Host analysis of a rowgroup-family plan (rowptr already on the host).
+int build_rowgroup_plan(csrspmm_plan_s* p, const std::vector<int>& rp, int n_hint, int vec) {
+  const int M = p->M, K = p->K, nnz = p->nnz;
+  int maxlen = 0;
+  for (int r = 0; r < M; ++r) maxlen = std::max(maxlen, rp[r + 1] - rp[r]);
+  p->maxlen = maxlen;
+  p->use_plan = ((long long)M + nnz >= kPlanMinItems) || maxlen > kSplitLen;
+  if (!p->use_plan) return 0;
+  p->nslots = nnz / kSplitLen;
+  p->nblocks = (int)(((long long)M + nnz + 1 + kMergeBlock - 1) / kMergeBlock);
+
+  // Panelized rows: long, on a large B, with non-decreasing columns.
+  // Only the float4 kernels gain: the scalar-column kernel (one 64-lane group
+  // per row) pays more per piece than it saves.
+  const int P = vec == 4 ? panel_count(K, n_hint) : 0;
+  std::vector<int> pan_rows;
+  std::vector<int> hcol;
+  std::vector<float> hval;
+  if (P > 0 && maxlen >= kPanelMinLen) {
+    hcol.resize((size_t)nnz);
+    hval.resize((size_t)nnz);
+    hipError_t e = hipMemcpy(hcol.data(), p->colidx, (size_t)nnz * sizeof(int), hipMemcpyDeviceToHost);
+    if (e == hipSuccess)
+      e = hipMemcpy(hval.data(), p->vals, (size_t)nnz * sizeof(float), hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return (int)e;
+    for (int r = 0; r < M; ++r) {
+      if (rp[r + 1] - rp[r] < kPanelMinLen) continue;
+      bool sorted = true;
+      for (int j = rp[r] + 1; j < rp[r + 1] && sorted; ++j) sorted = hcol[j - 1] <= hcol[j];
+      if (sorted) pan_rows.push_back(r);
+    }
+  }
+  std::vector<char> panelized((size_t)M, 0);
+  for (int r : pan_rows) panelized[r] = 1;
+
+  // Merge-block starts and segment slots: the formulas of plan_kernel, with
+  // panelized rows leaving their slots unused.
+  std::vector<int> block_start((size_t)p->nblocks + 1);
+  std::vector<int2> seg_info((size_t)p->nslots, make_int2(-1, 0));
+  long long fprev = -1;
+  for (int r = 0; r <= M; ++r) {
+    const long long f = (long long)r + rp[r];
+    const long long b_lo = fprev < 0 ? 0 : fprev / kMergeBlock + 1;
+    const long long b_hi = std::min(f / kMergeBlock, (long long)p->nblocks - 1);
+    for (long long b = b_lo; b <= b_hi; ++b) block_start[(size_t)b] = r;
+    fprev = f;
+    if (r == M) break;
+    const int len = rp[r + 1] - rp[r];
+    if (len > kSplitLen && !panelized[r]) {
+      const int s0 = rp[r] / kSplitLen;
+      for (int k = 0; k < len / kSplitLen; ++k) seg_info[(size_t)s0 + k] = make_int2(r, k);
+    }
+  }
+  block_start[(size_t)p->nblocks] = M;
+  hipError_t e = p->dev.alloc_copy(&p->d_block_start, block_start);
+  if (e == hipSuccess) e = p->dev.alloc_copy(&p->d_seg_info, seg_info);
+  if (e != hipSuccess) return (int)e;
+  if (pan_rows.empty()) return 0;
+
+  // Pieces: (row index i, panel, [a, b)) with b - a <= kSplitLen.
+  struct Piece {
+    int i, a, b;
+  };
+  const long long width = ((long long)K + P - 1) / P;
+  std::vector<std::vector<Piece>> by_panel((size_t)P);
+  for (int i = 0; i < (int)pan_rows.size(); ++i) {
+    const int r = pan_rows[(size_t)i];
+    int a = rp[r];
+    for (int pn = 0; pn < P; ++pn) {
+      const long long hi_col = (pn + 1) * width;
+      const int b = (int)(std::lower_bound(hcol.begin() + a, hcol.begin() + rp[r + 1], (int)std::min<long long>(hi_col, 0x7fffffff)) - hcol.begin());
+      for (int x = a; x < b; x += kSplitLen) by_panel[(size_t)pn].push_back({i, x, std::min(b, x + kSplitLen)});
+      a = b;
+    }
+  }
+  // Skewed columns (a few hot panels, as in R-MAT graphs) already give L2
+  // reuse without panels, and panels there only add partial traffic: keep
+  // such rows on the ordinary segment path.
+  std::vector<long long> weight((size_t)P, 0);
+  long long total = 0;
+  for (int pn = 0; pn < P; ++pn) {
+    for (const Piece& pc : by_panel[(size_t)pn]) weight[(size_t)pn] += pc.b - pc.a + 1;
+    total += weight[(size_t)pn];
+  }
+  if (*std::max_element(weight.begin(), weight.end()) * P > kPanelSkewMax * total) {
+    for (int r : pan_rows) {  // back to segments
+      const int len = rp[r + 1] - rp[r];
+      const int s0 = rp[r] / kSplitLen;
+      for (int k = 0; k < len / kSplitLen; ++k) seg_info[(size_t)s0 + k] = make_int2(r, k);
+    }
+    return to_status(hipMemcpy(p->d_seg_info, seg_info.data(), seg_info.size() * sizeof(int2),
+                               hipMemcpyHostToDevice));
+  }
+  // Panels go to XCDs in column order, each to the XCD with the least work so
+  // far; each XCD list keeps its panels in column order and is cut into units
+  // of ~kPanelUnitItems.
+  std::vector<std::vector<int>> panels_of(kXcds);
+  {
+    std::vector<long long> load(kXcds, 0);
+    for (int pn = 0; pn < P; ++pn) {
+      const int x = (int)(std::min_element(load.begin(), load.end()) - load.begin());
+      load[(size_t)x] += weight[(size_t)pn];
+      panels_of[(size_t)x].push_back(pn);
+    }
+  }
+  std::vector<std::vector<std::vector<Piece>>> units_of(kXcds);
+  for (int x = 0; x < kXcds; ++x) {
+    std::vector<Piece> cur;
+    int items = 0;
+    for (int pn : panels_of[(size_t)x]) {
+      for (const Piece& pc : by_panel[(size_t)pn]) {
+        cur.push_back(pc);
+        items += pc.b - pc.a + 1;
+        if (items >= kPanelUnitItems) {
+          units_of[x].push_back(cur);
+          cur.clear();
+          items = 0;
+        }
+      }
+    }
+    if (!cur.empty()) units_of[x].push_back(cur);
+  }
+  // Chunks of GPB units, XCD lists in turn; an exhausted list pads with
+  // empty units so every chunk keeps its XCD.
+  const int gpb = groups_per_block(vec, n_hint);
+  std::vector<int> drowptr(1, 0), dcol, unit_start(1, 0);
+  std::vector<float> dval;
+  std::vector<std::vector<std::pair<int, int>>> row_pieces(pan_rows.size());  // (CSR position, derived row)
+  std::vector<size_t> next(kXcds, 0);
+  bool more = true;
+  while (more) {
+    more = false;
+    for (int x = 0; x < kXcds; ++x) {
+      for (int u = 0; u < gpb; ++u) {
+        if (next[x] < units_of[x].size()) {
+          for (const Piece& pc : units_of[x][next[x]]) {
+            row_pieces[(size_t)pc.i].emplace_back(pc.a, (int)drowptr.size() - 1);
+            dcol.insert(dcol.end(), hcol.begin() + pc.a, hcol.begin() + pc.b);
+            dval.insert(dval.end(), hval.begin() + pc.a, hval.begin() + pc.b);
+            drowptr.push_back((int)dcol.size());
+          }
+          ++next[x];
+        }
+        unit_start.push_back((int)drowptr.size() - 1);
+      }
+    }
+    for (int x = 0; x < kXcds; ++x) more = more || next[x] < units_of[x].size();
+  }
+  // A row's pieces were appended XCD list by XCD list; the combine adds them
+  // in CSR order (sorted by their position in the original row).
+  std::vector<int> pan_ptr(1, 0), pan_piece;
+  for (auto& v : row_pieces) {
+    std::sort(v.begin(), v.end());
+    for (const auto& pr : v) pan_piece.push_back(pr.second);
+    pan_ptr.push_back((int)pan_piece.size());
+  }
+  p->npan = (int)pan_rows.size();
+  p->npieces = (int)drowptr.size() - 1;
+  p->nunits = (int)unit_start.size() - 1;
+  e = p->dev.alloc_copy(&p->d_pan_rows, pan_rows);
+  if (e == hipSuccess) e = p->dev.alloc_copy(&p->d_pan_ptr, pan_ptr);
+  if (e == hipSuccess) e = p->dev.alloc_copy(&p->d_pan_piece, pan_piece);
+  if (e == hipSuccess) e = p->dev.alloc_copy(&p->d_drowptr, drowptr);
+  if (e == hipSuccess) e = p->dev.alloc_copy(&p->d_dcolidx, dcol);
+  if (e == hipSuccess) e = p->dev.alloc_copy(&p->d_dvals, dval);
+  if (e == hipSuccess) e = p->dev.alloc_copy(&p->d_unit_start, unit_start);
+  return to_status(e);
+}
+
+}  // namespace
+
+extern "C" {
+
+int csrspmm_plan_create(int algo, int M, int K, int nnz, const int* rowptr, const int* colidx,
+                        const float* vals, int n_hint, void* stream, csrspmm_plan_t* out) {
+  if (!out) return CSRSPMM_STATUS_INVALID_VALUE;
+  *out = nullptr;
+  if (M < 0 || K < 0 || nnz < 0 || !rowptr || (nnz > 0 && (!colidx || !vals || K == 0)))
+    return CSRSPMM_STATUS_INVALID_VALUE;
+  if ((long long)M + nnz + 1 > 0x7fffffffLL - kMergeBlock) return CSRSPMM_STATUS_NOT_SUPPORTED;
+  const int n_eff = n_hint > 0 ? n_hint : 128;
+  const int concrete = resolve_algorithm(algo, n_eff);
+  if (concrete < 0) return CSRSPMM_STATUS_INVALID_VALUE;
+  hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));  // A must be ready
+  if (e != hipSuccess) return (int)e;
+  std::vector<int> rp((size_t)M + 1);
+  e = hipMemcpy(rp.data(), rowptr, rp.size() * sizeof(int), hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return (int)e;
+  if (rp[0] != 0 || rp[(size_t)M] != nnz) return CSRSPMM_STATUS_INVALID_CSR;
+  for (int r = 0; r < M; ++r)
+    if (rp[(size_t)r + 1] < rp[(size_t)r]) return CSRSPMM_STATUS_INVALID_CSR;
+  auto* p = new csrspmm_plan_s();
+  p->algo = concrete;
+  p->M = M;
+  p->K = K;
+  p->nnz = nnz;
+  p->rowptr = rowptr;
+  p->colidx = colidx;
+  p->vals = vals;
+  if (is_rowgroup_algorithm(concrete)) {
+    const int vec = (concrete == CSRSPMM_ALGO_WARP_PER_ROW_FP4 ||
+                     concrete == CSRSPMM_ALGO_WARP_PER_ROW_SMEM_FP4) && n_eff % 4 == 0 ? 4 : 1;
+    const int st = build_rowgroup_plan(p, rp, n_eff, vec);
+    if (st != 0) {
+      plan_free(p);
+      return st;
+    }
+    if (p->use_plan) {
+      e = ensure_partials(p, n_eff, static_cast<hipStream_t>(stream));
+      if (e != hipSuccess) {
+        plan_free(p);
+        return CSRSPMM_STATUS_ALLOC_FAILED;
+      }
+    }
+  }
+  *out = p;
+  return 0;
+}
+
+int csrspmm_plan_spmm_f32(csrspmm_plan_t plan, int N, const float* B, long long ldb, float* C,
+                          long long ldc, float alpha, float beta, unsigned flags, void* stream) {
+  if (!plan) return CSRSPMM_STATUS_INVALID_VALUE;
+  csrspmm_plan_s* p = plan;
+  if (!p->use_plan) {
+    // naive family or a small problem: the per-call path (allocates nothing)
+    return csrspmm_spmm_f32_ex(p->algo, p->M, p->K, N, p->nnz, p->rowptr, p->colidx, p->vals,
+                               p->maxlen, B, ldb, C, ldc, alpha, beta, flags, nullptr, 0, stream);
+  }
+  Problem pr{};
+  int st = fill_problem(pr, p->algo, p->M, p->K, N, p->nnz, p->rowptr, p->colidx, p->vals, B, ldb, C,
+                        ldc, alpha, beta, flags);
+  if (st != 0 || p->M == 0 || N == 0) return st;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = ensure_partials(p, N, s);
+  if (e != hipSuccess) return CSRSPMM_STATUS_ALLOC_FAILED;
+  pr.plan = true;
+  pr.plan_ready = true;
+  pr.nslots = p->nslots;
+  pr.nblocks = p->nblocks;
+  pr.block_start = p->d_block_start;
+  pr.seg_info = p->d_seg_info;
+  pr.partials = p->d_partials;
+  pr.ldp = p->ldp_cap;
+  pr.npan = p->npan;
+  pr.pan_rows = p->d_pan_rows;
+  pr.pan_ptr = p->d_pan_ptr;
+  pr.pan_piece = p->d_pan_piece;
+  pr.pan_part = p->d_pan_part;
+  const int vec = vector_width(p->algo, pr);
+  const bool lds = uses_lds(p->algo);
+  timing_before_main(s);
+  if (p->npan > 0) {
+    // the pieces of panelized rows, alone first so nothing else evicts their band
+    Problem d = pr;
+    d.M = p->npieces;
+    d.rowptr = p->d_drowptr;
+    d.colidx = p->d_dcolidx;
+    d.vals = p->d_dvals;
+    d.C = p->d_pan_part;
+    d.ldc = p->ldp_cap;
+    d.alpha = 1.0f;
+    d.beta = 0.0f;
+    d.epi = kEpiOverwrite;
+    d.nblocks = p->nunits;
+    d.block_start = p->d_unit_start;
+    d.nslots = 0;
+    d.npan = 0;
+    e = launch_rowgroup(d, vec, lds, s);
+  }
+  if (e == hipSuccess) e = launch_rowgroup(pr, vec, lds, s);
+  timing_after_main(s);
+  return to_status(e);
+}
+
+int csrspmm_plan_algorithm(csrspmm_plan_t plan) { return plan ? plan->algo : -1; }
+
+size_t csrspmm_plan_device_bytes(csrspmm_plan_t plan) {
+  return plan ? plan->dev.bytes + plan->partial_bytes : 0;
+}
+
+int csrspmm_plan_panelized_rows(csrspmm_plan_t plan) { return plan ? plan->npan : -1; }
+
+int csrspmm_plan_destroy(csrspmm_plan_t plan) {
+  if (!plan) return 0;
+  hipError_t e = hipDeviceSynchronize();  // no call may still use its buffers
+  plan_free(plan);
+  return to_status(e);
+}
+
+}  // extern "C"

@@ -315,27 +315,44 @@ __global__ __launch_bounds__(256) void combine_kernel(Problem p) {
   const int gl = lane & (GC - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nw = blockDim.x >> 6;
-  for (int s = blockIdx.x * nw + wave; s < p.nslots; s += gridDim.x * nw) {
-    const int2 si = p.seg_info[s];
-    if (si.x < 0 || si.x >= p.M || si.y != 0) continue;
-    const int nseg = (p.rowptr[si.x + 1] - p.rowptr[si.x]) / kSplitLen;
-    float* crow = p.C + (long long)si.x * p.ldc;
+  for (int s = blockIdx.x * nw + wave; s < p.nslots + p.npan; s += gridDim.x * nw) {
+    int row, nseg;
+    const float* base;
+    const int* pieces = nullptr;  // panelized row: partial index of each piece
+    if (s < p.nslots) {  // a split long row, found at its first slot
+      const int2 si = p.seg_info[s];
+      if (si.x < 0 || si.x >= p.M || si.y != 0) continue;
+      row = si.x;
+      nseg = (p.rowptr[row + 1] - p.rowptr[row]) / kSplitLen;
+      base = p.partials + (long long)s * p.ldp;
+    } else {  // a panelized row of a stored plan
+      const int i = s - p.nslots;
+      row = p.pan_rows[i];
+      nseg = p.pan_ptr[i + 1] - p.pan_ptr[i];
+      base = p.pan_part;
+      pieces = p.pan_piece + p.pan_ptr[i];
+    }
+    float* crow = p.C + (long long)row * p.ldc;
     for (int c0 = 0; c0 < p.N; c0 += GC * VEC) {
       const int c = c0 + gl * VEC;
       const bool cv = c < p.N;
-      const float* src = p.partials + (long long)s * p.ldp + c;
+      const float* src = base + c;
+      // partial k of this row
+      auto part = [&](int k) -> VT {
+        const long long idx = pieces ? (long long)pieces[k] : (long long)k;
+        return *reinterpret_cast<const VT*>(src + idx * p.ldp);
+      };
       VT acc = Vec<VEC>::zero();
       int k = q;
       for (; k + 3 * P < nseg; k += 4 * P) {
         VT a[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-          a[u] = cv ? *reinterpret_cast<const VT*>(src + (long long)(k + u * P) * p.ldp) : Vec<VEC>::zero();
+        for (int u = 0; u < 4; ++u) a[u] = cv ? part(k + u * P) : Vec<VEC>::zero();
 #pragma unroll
         for (int u = 0; u < 4; ++u) acc = add_v(acc, a[u]);
       }
       for (; k < nseg; k += P)
-        if (cv) acc = add_v(acc, *reinterpret_cast<const VT*>(src + (long long)k * p.ldp));
+        if (cv) acc = add_v(acc, part(k));
 #pragma unroll
       for (int off = GC; off < 64; off <<= 1) {
         if constexpr (VEC == 1) {
@@ -430,7 +447,7 @@ static hipError_t dispatch_vec1(const Problem& p, hipStream_t s) {
 
 hipError_t launch_rowgroup(const Problem& p, int vec, bool lds, hipStream_t s) {
   if (p.M == 0 || p.N == 0) return hipSuccess;
-  if (p.plan) {
+  if (p.plan && !p.plan_ready) {
     const int pblocks = std::min(div_up_host(p.M + 1, 256), 4096);
     hipLaunchKernelGGL(plan_kernel, dim3(pblocks), dim3(256), 0, s, p);
   }
@@ -441,8 +458,8 @@ hipError_t launch_rowgroup(const Problem& p, int vec, bool lds, hipStream_t s) {
     e = lds ? dispatch_vec1<true>(p, s) : dispatch_vec1<false>(p, s);
   }
   if (e != hipSuccess) return e;
-  if (p.plan && p.nslots > 0) {
-    const int cblocks = std::min(kPersistentBlocks, div_up_host(p.nslots, 4));
+  if (p.plan && p.nslots + p.npan > 0) {
+    const int cblocks = std::min(kPersistentBlocks, div_up_host(p.nslots + p.npan, 4));
     if (vec == 4) {
       launch_combine<4>(p, cblocks, s);
     } else {

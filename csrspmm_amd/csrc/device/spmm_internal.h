@@ -47,6 +47,10 @@ constexpr int kMergeBlock = CSRSPMM_MERGE_BLOCK;
 // processed whole by one group (one launch instead of three).
 constexpr long long kPlanMinItems = 1 << 16;
 
+// XCDs of an MI355X.  Workgroups are dispatched to them round-robin by
+// workgroup id, which stored plans use for L2 locality (plan.hip).
+constexpr int kXcds = 8;
+
 // Blocks of the persistent segment phase / combine phase: a few per CU.
 #ifndef CSRSPMM_PERSISTENT_BLOCKS
 #define CSRSPMM_PERSISTENT_BLOCKS 1024
@@ -73,6 +77,17 @@ struct Problem {
   int2* seg_info;     // per slot: (row, segment index) or (-1, 0) for an unused slot
   float* partials;    // nslots x ldp floats
   long long ldp;
+  // A stored plan (csrspmm_plan_create) filled block_start / seg_info once:
+  // no plan_kernel launch per call.
+  bool plan_ready;
+  // Panelized rows of a stored plan: row pan_rows[i] is summed in the combine
+  // pass from the partials pan_part[pan_piece[k] * ldp] of its pieces
+  // k in [pan_ptr[i], pan_ptr[i+1]), in column order.
+  int npan;
+  const int* pan_rows;
+  const int* pan_ptr;
+  const int* pan_piece;
+  const float* pan_part;
 };
 
 // Workspace layout for a problem (all offsets 256-byte aligned).
@@ -86,12 +101,24 @@ WorkspaceLayout workspace_layout(int M, int N, int nnz);
 // Bind the plan pointers of p into a workspace base pointer.
 void bind_workspace(Problem& p, void* ws, const WorkspaceLayout& L);
 
+// Shared by the per-call C ABI and stored plans (capi.hip).
+int resolve_algorithm(int algo, int N);  // CSRSPMM_ALGO_AUTO -> a concrete variant; -1 if invalid
+bool is_rowgroup_algorithm(int algo);
+bool uses_lds(int algo);
+int vector_width(int algo, const Problem& p);
+int fill_problem(Problem& p, int algo, int M, int K, int N, int nnz, const int* rowptr,
+                 const int* colidx, const float* vals, const float* B, long long ldb, float* C,
+                 long long ldc, float alpha, float beta, unsigned flags);
+hipError_t launch_algorithm(int algo, const Problem& p, hipStream_t s);
+
 hipError_t launch_naive(const Problem& p, hipStream_t s);
 hipError_t launch_naive_smem(const Problem& p, hipStream_t s);
 // vec = 1 (scalar columns) or 4 (float4 columns); lds = stage (col,val) in LDS.
 hipError_t launch_rowgroup(const Problem& p, int vec, bool lds, hipStream_t s);
 
 // Benchmark timing hook: no-ops unless csrspmm_timing_enable(1) was called.
+// Calls nest (per thread): only the outermost before/after pair records, so
+// one SpMM made of several launches is timed as one.
 void timing_before_main(hipStream_t s);
 void timing_after_main(hipStream_t s);
 

@@ -113,9 +113,140 @@ Tensor csrspmm_warp_per_row_smem_fp4_forward(Tensor A_row_ptr, Tensor A_col_idx,
                  static_cast<int>(std::min<int64_t>(A_max_row_nnz, INT32_MAX)), B, alpha, beta);
 }
 
+Tensor csrspmm_auto_forward(Tensor A_row_ptr, Tensor A_col_idx, Tensor A_values, Tensor B,
+                            double alpha, double beta) {
+  return forward(CSRSPMM_ALGO_AUTO, A_row_ptr, A_col_idx, A_values, -1, B, alpha, beta);
+}
+
+int algo_id(const std::string& name) {
+  const int a = csrspmm_parse_algorithm(name.c_str());
+  TORCH_CHECK(a >= 0, "unknown algorithm '", name, "'");
+  return a;
+}
+
+void check_out(const Tensor& C, const Tensor& B, int64_t M) {
+  TORCH_CHECK(C.is_cuda() && C.device() == B.device(), "C must be a CUDA tensor on B's device");
+  TORCH_CHECK(C.dtype() == torch::kFloat32, "C must be float32");
+  TORCH_CHECK(C.dim() == 2 && C.size(0) == M && C.size(1) == B.size(1), "C must be [M, N]");
+  TORCH_CHECK(C.size(1) <= 1 || C.stride(1) == 1, "C must be row-major (stride(1) == 1)");
+}
+
+long long ld_of(const Tensor& X) { return X.size(1) <= 1 ? std::max<int64_t>(X.size(1), 1) : X.stride(0); }
+
+// C = alpha * A * B + beta * C in place, with the prior C read when beta != 0
+// (the reference's C++ spmm() semantics, src/csrspmm.cpp:28-75; its torch
+// forwards always start from a fresh C).
+Tensor csrspmm_spmm_out(Tensor A_row_ptr, Tensor A_col_idx, Tensor A_values, Tensor B, Tensor C,
+                        double alpha_d, double beta_d, const std::string& algo) {
+  check_inputs(A_row_ptr, A_col_idx, A_values, B);
+  const int M = static_cast<int>(A_row_ptr.size(0) - 1);
+  check_out(C, B, M);
+  c10::DeviceGuard guard(B.device());
+  const int K = static_cast<int>(B.size(0)), N = static_cast<int>(B.size(1));
+  const int nnz = static_cast<int>(A_values.size(0));
+  if (M == 0 || N == 0) return C;
+  const int a = algo_id(algo);
+  const size_t ws_bytes = csrspmm_workspace_bytes(a, M, N, nnz);
+  Tensor ws;
+  if (ws_bytes > 0) ws = torch::empty({static_cast<int64_t>(ws_bytes)}, B.options().dtype(torch::kUInt8));
+  hipStream_t stream = c10::hip::getCurrentHIPStream(B.device().index()).stream();
+  const int st = csrspmm_spmm_f32_ex(a, M, K, N, nnz, A_row_ptr.data_ptr<int>(),
+                                     nnz ? A_col_idx.data_ptr<int>() : nullptr,
+                                     nnz ? A_values.data_ptr<float>() : nullptr, -1,
+                                     B.numel() ? B.data_ptr<float>() : nullptr, ld_of(B),
+                                     C.data_ptr<float>(), ld_of(C), static_cast<float>(alpha_d),
+                                     static_cast<float>(beta_d), 0u,
+                                     ws_bytes ? ws.data_ptr() : nullptr, ws_bytes, stream);
+  TORCH_CHECK(st == 0, "csrspmm_spmm_out failed: ", csrspmm_status_string(st));
+  return C;
+}
+
+// A stored plan (csrspmm_plan_*) for one CSR matrix; holds references to the
+// CSR tensors, which the plan reads in place.
+class CsrSpmmPlan {
+ public:
+  CsrSpmmPlan(Tensor rowptr, Tensor colidx, Tensor vals, int64_t K, const std::string& algo,
+              int64_t n_hint)
+      : rowptr_(rowptr), colidx_(colidx), vals_(vals), K_(K) {
+    TORCH_CHECK(rowptr.is_cuda() && colidx.is_cuda() && vals.is_cuda(),
+                "CSR tensors must be CUDA tensors");
+    TORCH_CHECK(rowptr.dtype() == torch::kInt32, "A_row_ptr must be int32");
+    TORCH_CHECK(colidx.dtype() == torch::kInt32, "A_col_idx must be int32");
+    TORCH_CHECK(vals.dtype() == torch::kFloat32, "A_values must be float32");
+    TORCH_CHECK(rowptr.dim() == 1 && rowptr.size(0) >= 1 && colidx.dim() == 1 && vals.dim() == 1 &&
+                    colidx.size(0) == vals.size(0),
+                "bad CSR shapes");
+    TORCH_CHECK(rowptr.is_contiguous() && colidx.is_contiguous() && vals.is_contiguous(),
+                "CSR arrays must be contiguous");
+    TORCH_CHECK(K >= 0 && K <= INT32_MAX && vals.size(0) <= INT32_MAX, "sizes must fit int32");
+    c10::DeviceGuard guard(rowptr.device());
+    const int nnz = static_cast<int>(vals.size(0));
+    hipStream_t stream = c10::hip::getCurrentHIPStream(rowptr.device().index()).stream();
+    const int st = csrspmm_plan_create(algo_id(algo), static_cast<int>(rowptr.size(0) - 1),
+                                       static_cast<int>(K), nnz, rowptr.data_ptr<int>(),
+                                       nnz ? colidx.data_ptr<int>() : nullptr,
+                                       nnz ? vals.data_ptr<float>() : nullptr,
+                                       static_cast<int>(n_hint), stream, &plan_);
+    TORCH_CHECK(st == 0, "csrspmm_plan_create failed: ", csrspmm_status_string(st));
+  }
+  ~CsrSpmmPlan() {
+    if (plan_) (void)csrspmm_plan_destroy(plan_);
+  }
+  CsrSpmmPlan(const CsrSpmmPlan&) = delete;
+  CsrSpmmPlan& operator=(const CsrSpmmPlan&) = delete;
+
+  // New [M, N] output, the reference forwards' semantics (beta scales zero).
+  Tensor spmm(Tensor B, double alpha, double beta) {
+    check_b(B);
+    Tensor C = torch::empty({rowptr_.size(0) - 1, B.size(1)}, B.options());
+    run(B, C, alpha, beta, beta != 0.0 ? CSRSPMM_FLAG_C_IS_ZERO : 0u);
+    return C;
+  }
+  // In place: C = alpha * A * B + beta * C.
+  Tensor spmm_out(Tensor B, Tensor C, double alpha, double beta) {
+    check_b(B);
+    check_out(C, B, rowptr_.size(0) - 1);
+    run(B, C, alpha, beta, 0u);
+    return C;
+  }
+  std::string algorithm() const { return csrspmm_algorithm_name(csrspmm_plan_algorithm(plan_)); }
+  int64_t device_bytes() const { return static_cast<int64_t>(csrspmm_plan_device_bytes(plan_)); }
+  int64_t panelized_rows() const { return csrspmm_plan_panelized_rows(plan_); }
+
+ private:
+  void check_b(const Tensor& B) const {
+    TORCH_CHECK(B.is_cuda() && B.device() == rowptr_.device(), "B must be a CUDA tensor on A's device");
+    TORCH_CHECK(B.dtype() == torch::kFloat32, "B must be float32");
+    TORCH_CHECK(B.dim() == 2 && B.size(0) == K_, "B must be [K, N]");
+    TORCH_CHECK(B.size(1) <= 1 || B.stride(1) == 1, "B must be row-major (stride(1) == 1)");
+  }
+  void run(const Tensor& B, Tensor& C, double alpha, double beta, unsigned flags) {
+    c10::DeviceGuard guard(B.device());
+    if (C.numel() == 0) return;
+    hipStream_t stream = c10::hip::getCurrentHIPStream(B.device().index()).stream();
+    const int st = csrspmm_plan_spmm_f32(plan_, static_cast<int>(B.size(1)),
+                                         B.numel() ? B.data_ptr<float>() : nullptr, ld_of(B),
+                                         C.data_ptr<float>(), ld_of(C), static_cast<float>(alpha),
+                                         static_cast<float>(beta), flags, stream);
+    TORCH_CHECK(st == 0, "csrspmm plan spmm failed: ", csrspmm_status_string(st));
+  }
+  Tensor rowptr_, colidx_, vals_;
+  int64_t K_;
+  csrspmm_plan_t plan_ = nullptr;
+};
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.def("csrspmm_auto", &csrspmm_auto_forward, "CSR SpMM (variant picked from N)");
+  m.def("csrspmm_spmm_out", &csrspmm_spmm_out, "CSR SpMM into C in place (C = alpha*A*B + beta*C)");
+  pybind11::class_<CsrSpmmPlan>(m, "CsrSpmmPlan")
+      .def(pybind11::init<Tensor, Tensor, Tensor, int64_t, const std::string&, int64_t>())
+      .def("spmm", &CsrSpmmPlan::spmm)
+      .def("spmm_out", &CsrSpmmPlan::spmm_out)
+      .def_property_readonly("algorithm", &CsrSpmmPlan::algorithm)
+      .def_property_readonly("device_bytes", &CsrSpmmPlan::device_bytes)
+      .def_property_readonly("panelized_rows", &CsrSpmmPlan::panelized_rows);
   m.def("csrspmm_naive", &csrspmm_naive_forward, "CSR SpMM (naive)");
   m.def("csrspmm_warp_per_row", &csrspmm_warp_per_row_forward, "CSR SpMM (warp_per_row)");
   m.def("csrspmm_warp_per_row_smem", &csrspmm_warp_per_row_smem_forward,

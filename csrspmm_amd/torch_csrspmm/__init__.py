@@ -26,6 +26,9 @@ __all__ = [
     "csrspmm_warp_per_row_fp4",
     "csrspmm_warp_per_row_smem_fp4",
 ]
+# Beyond the reference's five: the variant picked from N, an in-place product
+# with a real beta, and a stored plan for repeated products with one A.
+EXTRAS = ["csrspmm_auto", "csrspmm_spmm_out", "CsrSpmmPlan"]
 
 
 def csrspmm_naive(A_rowptr, A_colidx, A_values, B, alpha, beta):
@@ -47,3 +50,46 @@ def csrspmm_warp_per_row_fp4(A_rowptr, A_colidx, A_values, B, alpha, beta):
 def csrspmm_warp_per_row_smem_fp4(A_rowptr, A_colidx, A_values, A_max_row_nnz, B, alpha, beta):
     return _C.csrspmm_warp_per_row_smem_fp4(A_rowptr, A_colidx, A_values, A_max_row_nnz, B, alpha,
                                             beta)
+
+
+def csrspmm_auto(A_rowptr, A_colidx, A_values, B, alpha, beta):
+    """As the five entry points, with the variant picked from N."""
+    return _C.csrspmm_auto(A_rowptr, A_colidx, A_values, B, alpha, beta)
+
+
+def csrspmm_spmm_out(A_rowptr, A_colidx, A_values, B, C, alpha, beta, algo="Auto"):
+    """C = alpha * A @ B + beta * C in place (C is read when beta != 0); returns C."""
+    return _C.csrspmm_spmm_out(A_rowptr, A_colidx, A_values, B, C, alpha, beta, algo)
+
+
+class CsrSpmmPlan:
+    """A stored plan for repeated products with one CSR matrix A (K columns).
+
+        plan = CsrSpmmPlan(rowptr, colidx, values, K)        # algo="Auto"
+        C = plan.spmm(B, alpha, beta)          # new C, like the entry points
+        plan.spmm_out(B, C, alpha, beta)       # in place, C = alpha*A@B + beta*C
+
+    The CSR tensors are used in place and must not be modified while the
+    plan is alive; n_hint is the expected number of columns of B.
+    """
+
+    def __init__(self, A_rowptr, A_colidx, A_values, K, algo="Auto", n_hint=0):
+        self._plan = _C.CsrSpmmPlan(A_rowptr, A_colidx, A_values, int(K), algo, int(n_hint))
+
+    def spmm(self, B, alpha=1.0, beta=0.0):
+        return self._plan.spmm(B, alpha, beta)
+
+    def spmm_out(self, B, C, alpha=1.0, beta=0.0):
+        return self._plan.spmm_out(B, C, alpha, beta)
+
+    @property
+    def algorithm(self):
+        return self._plan.algorithm
+
+    @property
+    def device_bytes(self):
+        return self._plan.device_bytes
+
+    @property
+    def panelized_rows(self):
+        return self._plan.panelized_rows

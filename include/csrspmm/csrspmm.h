@@ -6,20 +6,25 @@
 #include <csrspmm/csr_utils.h>
 #include <csrspmm/matrix.h>
 
+struct csrspmm_plan_s;  // opaque plan of the C ABI (include/csrspmm_c.h)
+
 namespace csrspmm {
 
-// Same enumerators in the same order as the reference (csrspmm.h:10-17).
+// The reference's enumerators in the reference's order (csrspmm.h:10-17),
+// then Auto, which picks a variant from N (the reference's spmm() has only an
+// "auto-selection" stub that always runs Naive, src/csrspmm.cpp:34-40).
 enum class Algorithm {
     Naive,
     NaiveSmem,
     WarpPerRow,
     WarpPerRowFp4,
     WarpPerRowSmem,
-    WarpPerRowSmemFp4
+    WarpPerRowSmemFp4,
+    Auto
 };
 
-// Exact CamelCase match; an unknown name prints a warning to stderr and
-// returns Naive (reference src/csrspmm.cpp:13-25).
+// Exact CamelCase match ("Auto" included); an unknown name prints a warning
+// to stderr and returns Naive (reference src/csrspmm.cpp:13-25).
 Algorithm parse_algorithm(const std::string& name);
 
 // C = alpha * A * B + beta * C on the device.
@@ -33,5 +38,33 @@ void spmm(const CSRMatrix& A,
           DenseMatrix& C,
           float alpha, float beta,
           Algorithm algo = Algorithm::Naive);
+
+// A stored plan for repeated products with one device CSR matrix A
+// (include/csrspmm_c.h, csrspmm_plan_*): analysed once, including the
+// column-panel layout of very long rows that speeds up large, skew-free
+// matrices.  A's arrays must outlive the plan and stay unchanged.  Errors
+// print a message and exit, like the rest of this API.
+class SpmmPlan {
+public:
+    explicit SpmmPlan(const CSRMatrix& A, Algorithm algo = Algorithm::Auto, int n_hint = 0);
+    ~SpmmPlan();
+    SpmmPlan(const SpmmPlan&) = delete;
+    SpmmPlan& operator=(const SpmmPlan&) = delete;
+    SpmmPlan(SpmmPlan&& other) noexcept;
+    SpmmPlan& operator=(SpmmPlan&& other) noexcept;
+
+    // C = alpha * A * B + beta * C; returns after the device has finished,
+    // like spmm().
+    void run(const DenseMatrix& B, DenseMatrix& C, float alpha, float beta);
+    // The same, enqueued on the default stream without waiting.
+    void run_async(const DenseMatrix& B, DenseMatrix& C, float alpha, float beta);
+
+    Algorithm algorithm() const;     // the concrete variant the plan runs
+    size_t device_bytes() const;     // device memory the plan holds
+    int panelized_rows() const;      // rows laid out in column panels
+
+private:
+    ::csrspmm_plan_s* plan_ = nullptr;
+};
 
 }  // namespace csrspmm

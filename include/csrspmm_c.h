@@ -33,7 +33,10 @@ enum {
     CSRSPMM_ALGO_WARP_PER_ROW_FP4 = 3,
     CSRSPMM_ALGO_WARP_PER_ROW_SMEM = 4,
     CSRSPMM_ALGO_WARP_PER_ROW_SMEM_FP4 = 5,
-    CSRSPMM_ALGO_COUNT = 6
+    CSRSPMM_ALGO_COUNT = 6,   /* number of concrete variants */
+    /* Pick a variant from the problem (csrspmm_resolve_algorithm).  Fills the
+     * reference's "auto-selection" stub (src/csrspmm.cpp:34-40). */
+    CSRSPMM_ALGO_AUTO = 6
 };
 
 enum {
@@ -69,8 +72,12 @@ const char* csrspmm_status_string(int status);
  * (reference src/csrspmm.cpp:13-25). */
 int csrspmm_parse_algorithm(const char* name);
 
-/* Algorithm id -> CamelCase name, or NULL for an unknown id. */
+/* Algorithm id -> CamelCase name ("Auto" for CSRSPMM_ALGO_AUTO), or NULL. */
 const char* csrspmm_algorithm_name(int algo);
+
+/* The concrete variant CSRSPMM_ALGO_AUTO runs for N output columns (a
+ * concrete id is returned unchanged; -1 for an invalid id). */
+int csrspmm_resolve_algorithm(int algo, int N);
 
 /* Bytes of device workspace csrspmm_spmm_f32_ws needs for this problem
  * (row-split plan, partial sums of split rows, counters).  No counterpart in
@@ -126,6 +133,49 @@ int csrspmm_spmm_f32_ex(int algo, int M, int K, int N, int nnz,
                         unsigned flags,
                         void* workspace, size_t workspace_bytes,
                         void* stream);
+
+/*
+ * Stored plans: analyse A once, then multiply it by many B.  No counterpart
+ * in the reference, whose spmm() re-derives nothing between calls
+ * (src/csrspmm.cpp:28-75); its "auto-selection" stub (:34-40) is what
+ * CSRSPMM_ALGO_AUTO fills.
+ *
+ * csrspmm_plan_create synchronises `stream`, reads rowptr (and, for
+ * very long rows on a large B, their columns and values) to the host, and
+ * keeps on the device:
+ *  - the merge-block starts and long-row segment slots (no per-call plan
+ *    kernel);
+ *  - for rows of >= 2048 nonzeros with sorted columns when K*N*4 >= 16 MiB, a
+ *    column-panel copy of the row pieces, laid out so that each of the 8 XCDs
+ *    streams its own panels in order and keeps the gathered B band in its L2;
+ *  - partial-sum buffers for n_hint columns (grown on a call with larger N).
+ * n_hint <= 0 means 128.  The CSR arrays are referenced, not copied (except
+ * the panel pieces): they must stay alive and unchanged while the plan is
+ * used.  A plan serves one stream at a time (its partial buffers are shared
+ * by its calls).  Creation and destruction allocate and synchronise; calls
+ * allocate only when N outgrows the buffers.
+ */
+typedef struct csrspmm_plan_s* csrspmm_plan_t;
+
+int csrspmm_plan_create(int algo, int M, int K, int nnz,
+                        const int* rowptr, const int* colidx, const float* vals,
+                        int n_hint, void* stream, csrspmm_plan_t* plan);
+
+/* C = alpha * A * B + beta * C with the plan's A; flags as for
+ * csrspmm_spmm_f32_ex.  Asynchronous on `stream`. */
+int csrspmm_plan_spmm_f32(csrspmm_plan_t plan, int N,
+                          const float* B, long long ldb,
+                          float* C, long long ldc,
+                          float alpha, float beta, unsigned flags, void* stream);
+
+/* The concrete variant the plan runs. */
+int csrspmm_plan_algorithm(csrspmm_plan_t plan);
+/* Device memory the plan holds, in bytes. */
+size_t csrspmm_plan_device_bytes(csrspmm_plan_t plan);
+/* Rows the plan cut into column panels. */
+int csrspmm_plan_panelized_rows(csrspmm_plan_t plan);
+/* Waits for the device, then frees the plan (NULL is a no-op). */
+int csrspmm_plan_destroy(csrspmm_plan_t plan);
 
 /* Device-side CSR validation.  Writes the CSRSPMM_CSR_* bit set to
  * *flags_out and the true longest row to *max_row_nnz_out (host pointers,

@@ -31,6 +31,8 @@ static int checks() {
   CHECK(parse_algorithm("WarpPerRowFp4") == Algorithm::WarpPerRowFp4);
   CHECK(parse_algorithm("WarpPerRowSmem") == Algorithm::WarpPerRowSmem);
   CHECK(parse_algorithm("WarpPerRowSmemFp4") == Algorithm::WarpPerRowSmemFp4);
+  CHECK(parse_algorithm("Auto") == Algorithm::Auto);
+  CHECK(static_cast<int>(Algorithm::WarpPerRowSmemFp4) == 5 && static_cast<int>(Algorithm::Auto) == 6);
   CHECK(parse_algorithm("adaptive") == Algorithm::Naive);  // warns on stderr, falls back
   CHECK(WARP_SIZE == 64);
 

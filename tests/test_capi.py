@@ -40,7 +40,16 @@ def test_parse_and_names():
     assert lib.csrspmm_parse_algorithm(b"naive") == -1  # exact CamelCase match only
     assert lib.csrspmm_parse_algorithm(b"Adaptive") == -1
     assert lib.csrspmm_parse_algorithm(None) == -1
-    assert lib.csrspmm_algorithm_name(6) is None
+    assert lib.csrspmm_parse_algorithm(b"Auto") == 6
+    assert lib.csrspmm_algorithm_name(6).decode() == "Auto"
+    assert lib.csrspmm_algorithm_name(7) is None
+    # Auto resolves by N; concrete ids pass through
+    assert lib.csrspmm_resolve_algorithm(6, 128) == 5
+    assert lib.csrspmm_resolve_algorithm(6, 256) == 5
+    assert lib.csrspmm_resolve_algorithm(6, 64) == 4
+    assert lib.csrspmm_resolve_algorithm(6, 130) == 4
+    assert lib.csrspmm_resolve_algorithm(2, 128) == 2
+    assert lib.csrspmm_resolve_algorithm(9, 128) == -1
     assert lib.csrspmm_version() >= 100
 
 
@@ -103,6 +112,21 @@ def test_ex_rejects_small_workspace_without_device():
     st = lib.csrspmm_spmm_f32_ex(3, 262144, 262144, 128, 8453223, fake, fake, fake, -1, fake, 128,
                                  fake, 128, 1.0, 0.0, 0, fake + 8, need, None)
     assert st == -1  # misaligned workspace
+
+
+def test_plan_argument_errors_without_device():
+    import ctypes
+    lib = capi.hip()
+    h = ctypes.c_void_p()
+    assert lib.csrspmm_plan_create(3, 4, 4, 0, None, None, None, 0, None, ctypes.byref(h)) == -1
+    assert lib.csrspmm_plan_create(3, -1, 4, 0, 0x1000, None, None, 0, None, ctypes.byref(h)) == -1
+    assert lib.csrspmm_plan_create(3, 4, 4, 5, 0x1000, None, None, 0, None, ctypes.byref(h)) == -1
+    assert lib.csrspmm_plan_create(9, 4, 4, 0, 0x1000, None, None, 0, None, ctypes.byref(h)) == -1
+    assert lib.csrspmm_plan_create(3, 4, 4, 0, 0x1000, None, None, 0, None, None) == -1
+    assert lib.csrspmm_plan_spmm_f32(None, 4, None, 4, None, 4, 1.0, 0.0, 0, None) == -1
+    assert lib.csrspmm_plan_algorithm(None) == -1
+    assert lib.csrspmm_plan_device_bytes(None) == 0
+    assert lib.csrspmm_plan_destroy(None) == 0
 
 
 def test_validate_rejects_bad_sizes_without_device():

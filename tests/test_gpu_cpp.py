@@ -23,7 +23,8 @@ def test_cpp_test_driver_all_variants(args, gpu):
                        capture_output=True, text=True, timeout=120)
     print(r.stdout, r.stderr)
     assert r.returncode == 0
-    assert r.stdout.count("Pass: ") == 6
+    assert r.stdout.count("Pass: ") == 14  # 7 algorithms, each per call and through a plan
+    assert "Error" not in r.stdout
 
 
 def test_cpp_bench_driver(gpu):

@@ -112,3 +112,50 @@ def test_xl_through_torch(gpu):
     R, S = oracle.spmm_f64(a.rowptr, a.colidx, a.vals, B, rows=rows)
     bad, ratio, _, _ = oracle.check(C.cpu().numpy()[rows], R, S, 1e-5)
     assert bad == 0, ratio
+
+
+def test_auto_and_spmm_out(gpu):
+    rng = np.random.default_rng(11)
+    rp, ci, va, mx = random_csr(500, 300, 0.1, rng)
+    t = lambda x: torch.from_numpy(x).to(gpu)  # noqa: E731
+    for N in (8, 64, 200, 256):
+        B = rng.standard_normal((300, N)).astype(np.float32)
+        C = tc.csrspmm_auto(t(rp), t(ci), t(va), t(B), 0.75, 3.0)
+        check("auto", C, rp, ci, va, B, 0.75, 3.0)
+        C0 = rng.standard_normal((500, N)).astype(np.float32)
+        for algo in ("Auto", "Naive", "WarpPerRowFp4", "WarpPerRowSmem"):
+            dC = t(C0)
+            out = tc.csrspmm_spmm_out(t(rp), t(ci), t(va), t(B), dC, 0.5, -1.25, algo=algo)
+            assert out.data_ptr() == dC.data_ptr()
+            R, S = oracle.spmm_f64(rp, ci, va, B, C0, 0.5, -1.25)
+            bad, ratio, _, _ = oracle.check(dC.cpu().numpy(), R, S, 1e-5)
+            assert bad == 0, f"spmm_out {algo} N={N}: {ratio}"
+    B = t(rng.standard_normal((300, 16)).astype(np.float32))
+    with pytest.raises(RuntimeError, match=r"C must be \[M, N\]"):
+        tc.csrspmm_spmm_out(t(rp), t(ci), t(va), B, torch.zeros(499, 16, device=gpu), 1.0, 0.0)
+    with pytest.raises(RuntimeError, match="unknown algorithm"):
+        tc.csrspmm_spmm_out(t(rp), t(ci), t(va), B, torch.zeros(500, 16, device=gpu), 1.0, 0.0,
+                            algo="Fastest")
+
+
+def test_plan_class(gpu):
+    cfg = configs.CONFIGS["xl"]
+    a = cfg.csr()
+    B = cfg.B(a.K)
+    t = lambda x: torch.from_numpy(x).to(gpu)  # noqa: E731
+    plan = tc.CsrSpmmPlan(t(a.rowptr), t(a.colidx), t(a.vals), a.K, n_hint=cfg.N)
+    assert plan.algorithm == "WarpPerRowSmemFp4" and plan.panelized_rows > 0
+    assert plan.device_bytes > 0
+    rows = np.unique(np.concatenate([np.argsort(np.diff(a.rowptr))[-32:],
+                                     np.arange(0, a.M, 97)])).astype(np.int32)
+    dB = t(B)
+    C = plan.spmm(dB, 1.0, 0.0)
+    R, S = oracle.spmm_f64(a.rowptr, a.colidx, a.vals, B, rows=rows)
+    bad, ratio, _, _ = oracle.check(C.cpu().numpy()[rows], R, S, 1e-5)
+    assert bad == 0, ratio
+    C2 = plan.spmm(dB, 1.0, 5.0)  # beta scales a zero C, as the forwards
+    assert torch.equal(C, C2)
+    plan.spmm_out(dB, C2, 1.0, -1.0)  # C - A*B: exactly zero per element
+    assert float(C2.abs().max()) == 0.0
+    with pytest.raises(RuntimeError, match=r"B must be \[K, N\]"):
+        plan.spmm(dB[:-1], 1.0, 0.0)

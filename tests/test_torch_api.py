@@ -22,6 +22,8 @@ SIGS = {
 
 def test_entry_points_and_signatures():
     assert sorted(tc.__all__) == sorted(SIGS)
+    for name in tc.EXTRAS:
+        assert hasattr(tc, name)
     for name, params in SIGS.items():
         assert list(inspect.signature(getattr(tc, name)).parameters) == params
         assert hasattr(tc._C, name)
@@ -43,3 +45,13 @@ def test_host_tensors_raise(name):
     args = (rowptr, colidx, vals, 1, B, 1.0, 0.0) if "smem" in name else (rowptr, colidx, vals, B, 1.0, 0.0)
     with pytest.raises(RuntimeError, match="A_row_ptr must be a CUDA tensor"):
         fn(*args)
+
+
+def test_extras_raise_on_host_tensors():
+    rowptr, colidx, vals, B = cpu_inputs()
+    with pytest.raises(RuntimeError, match="A_row_ptr must be a CUDA tensor"):
+        tc.csrspmm_auto(rowptr, colidx, vals, B, 1.0, 0.0)
+    with pytest.raises(RuntimeError, match="A_row_ptr must be a CUDA tensor"):
+        tc.csrspmm_spmm_out(rowptr, colidx, vals, B, torch.zeros(2, 4), 1.0, 0.0)
+    with pytest.raises(RuntimeError, match="CSR tensors must be CUDA tensors"):
+        tc.CsrSpmmPlan(rowptr, colidx, vals, 2)
