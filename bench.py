@@ -10,6 +10,10 @@ stream.  Prints ONE JSON line:
   roofline   achieved gather-model GB/s of the main kernel (HIP event pair
              around it, csrspmm_timing_*) against 8 TB/s
   variants   the same figures for every variant on the same config
+  plan       the same figures for a stored plan (csrspmm_plan_*, Auto by
+             default) built once outside the timed region, with its build
+             time; the headline stays the per-call path, which needs no
+             preprocessing of A
   cpu_baseline  the fp32 CSR restatement (oracle/cpu_spmm.c) on the host
              cores, full matrix, median of a bounded number of reps
 The default config is the XL power-law matrix the north-star target is
@@ -40,6 +44,7 @@ def parse():
     ap.add_argument("--algo", default="WarpPerRowFp4")
     ap.add_argument("--variants", default="all", help="'all', 'none' or comma list")
     ap.add_argument("--variant-steps", type=int, default=20)
+    ap.add_argument("--plan-algo", default="Auto", help="stored-plan leg ('none' disables it)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="time budget of the CPU baseline leg (0 disables it)")
     ap.add_argument("--traffic-file", default=os.path.join(HERE, "profiles", "traffic.json"))
@@ -68,6 +73,31 @@ def time_variant(capi, torch, algo, d, steps, warmup):
     main_ms, calls = capi.timing_read()
     total_ms = start.elapsed_time(stop)
     return total_ms / steps, main_ms / max(calls, 1)
+
+
+def time_plan(capi, torch, algo, d, K, N, steps, warmup):
+    """(plan object, build ms, ms per call, main-kernel ms per call)."""
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    plan = capi.Plan(algo, d["rowptr"], d["colidx"], d["vals"], K, n_hint=N)
+    torch.cuda.synchronize()
+    build_ms = (time.perf_counter() - t0) * 1e3
+    for _ in range(warmup):
+        plan.spmm(d["B"], d["C"], 1.0, 0.0)
+    torch.cuda.synchronize()
+    capi.timing_read()
+    capi.timing_enable(True)
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    stream = torch.cuda.current_stream()
+    start.record(stream)
+    for _ in range(steps):
+        plan.spmm(d["B"], d["C"], 1.0, 0.0)
+    stop.record(stream)
+    torch.cuda.synchronize()
+    capi.timing_enable(False)
+    main_ms, calls = capi.timing_read()
+    return plan, build_ms, start.elapsed_time(stop) / steps, main_ms / max(calls, 1)
 
 
 def cpu_baseline(a, B, budget_s):
@@ -160,6 +190,17 @@ def main():
             variants[name] = figures(vms, vmain)
             print(f"[bench] {name}: {vms:.4f} ms/call", file=sys.stderr, flush=True)
 
+    plan_fig = None
+    if args.plan_algo != "none":
+        plan, build_ms, pms, pmain = time_plan(capi, torch, args.plan_algo, d, a.K, N,
+                                               args.variant_steps, 3)
+        plan_fig = {"algo": args.plan_algo, "resolved": plan.algorithm, **figures(pms, pmain),
+                    "build_ms": round(build_ms, 2), "device_bytes": plan.device_bytes,
+                    "panelized_rows": plan.panelized_rows}
+        plan.close()
+        print(f"[bench] plan {plan_fig['resolved']}: {pms:.4f} ms/call, main {pmain:.4f} ms, "
+              f"built in {build_ms:.1f} ms", file=sys.stderr, flush=True)
+
     traffic = None
     if os.path.exists(args.traffic_file):
         with open(args.traffic_file) as f:
@@ -196,6 +237,7 @@ def main():
                      "kernel_ms": round(main_ms, 5)},
         "cpu_baseline": cpu,
         "variants": variants,
+        "plan": plan_fig,
     }
     print(json.dumps(out), flush=True)
 

@@ -20,7 +20,7 @@ static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 WorkspaceLayout workspace_layout(int M, int N, int nnz) {
   WorkspaceLayout L{};
-  L.nslots = nnz / kSplitLen;
+  L.nslots = nnz / kSegLen;
   L.nblocks = (int)(((long long)M + nnz + 1 + kMergeBlock - 1) / kMergeBlock);
   L.ldp = ((long long)N + 3) & ~3LL;
   size_t off = 0;
@@ -56,7 +56,7 @@ bool is_rowgroup(int algo) {
 bool wants_plan(int algo, int M, int nnz, int hint) {
   if (!is_rowgroup(algo)) return false;
   if ((long long)M + nnz >= kPlanMinItems) return true;
-  return (hint < 0 || hint > kSplitLen) && nnz > kSplitLen;
+  return (hint < 0 || hint > kLongRow) && nnz > kLongRow;
 }
 
 int to_status(hipError_t e) { return e == hipSuccess ? 0 : (int)e; }

@@ -7,7 +7,7 @@
 //
 // Panelized rows.  A row of at least kPanelMinLen nonzeros with sorted
 // columns is cut at column-panel boundaries (P panels of K/P columns, the
-// B band of a panel is ~kPanelBandBytes) into pieces of at most kSplitLen
+// B band of a panel is ~kPanelBandBytes) into pieces of at most kLongRow
 // nonzeros.  Panels are dealt to the 8 XCDs in column order, each to the
 // least-loaded XCD; the pieces of an XCD's panels, in panel order, form its
 // list, and each list is cut into units of ~kPanelUnitItems
@@ -157,9 +157,9 @@ int build_rowgroup_plan(csrspmm_plan_s* p, const std::vector<int>& rp, int n_hin
   int maxlen = 0;
   for (int r = 0; r < M; ++r) maxlen = std::max(maxlen, rp[r + 1] - rp[r]);
   p->maxlen = maxlen;
-  p->use_plan = ((long long)M + nnz >= kPlanMinItems) || maxlen > kSplitLen;
+  p->use_plan = ((long long)M + nnz >= kPlanMinItems) || maxlen > kLongRow;
   if (!p->use_plan) return 0;
-  p->nslots = nnz / kSplitLen;
+  p->nslots = nnz / kSegLen;
   p->nblocks = (int)(((long long)M + nnz + 1 + kMergeBlock - 1) / kMergeBlock);
 
   // Panelized rows: long, on a large B, with non-decreasing columns.
@@ -199,9 +199,9 @@ int build_rowgroup_plan(csrspmm_plan_s* p, const std::vector<int>& rp, int n_hin
     fprev = f;
     if (r == M) break;
     const int len = rp[r + 1] - rp[r];
-    if (len > kSplitLen && !panelized[r]) {
-      const int s0 = rp[r] / kSplitLen;
-      for (int k = 0; k < len / kSplitLen; ++k) seg_info[(size_t)s0 + k] = make_int2(r, k);
+    if (len > kLongRow && !panelized[r]) {
+      const int s0 = rp[r] / kSegLen;
+      for (int k = 0; k < len / kSegLen; ++k) seg_info[(size_t)s0 + k] = make_int2(r, k);
     }
   }
   block_start[(size_t)p->nblocks] = M;
@@ -210,7 +210,7 @@ int build_rowgroup_plan(csrspmm_plan_s* p, const std::vector<int>& rp, int n_hin
   if (e != hipSuccess) return (int)e;
   if (pan_rows.empty()) return 0;
 
-  // Pieces: (row index i, panel, [a, b)) with b - a <= kSplitLen.
+  // Pieces: (row index i, panel, [a, b)) with b - a <= kLongRow.
   struct Piece {
     int i, a, b;
   };
@@ -222,7 +222,7 @@ int build_rowgroup_plan(csrspmm_plan_s* p, const std::vector<int>& rp, int n_hin
     for (int pn = 0; pn < P; ++pn) {
       const long long hi_col = (pn + 1) * width;
       const int b = (int)(std::lower_bound(hcol.begin() + a, hcol.begin() + rp[r + 1], (int)std::min<long long>(hi_col, 0x7fffffff)) - hcol.begin());
-      for (int x = a; x < b; x += kSplitLen) by_panel[(size_t)pn].push_back({i, x, std::min(b, x + kSplitLen)});
+      for (int x = a; x < b; x += kLongRow) by_panel[(size_t)pn].push_back({i, x, std::min(b, x + kLongRow)});
       a = b;
     }
   }
@@ -238,8 +238,8 @@ int build_rowgroup_plan(csrspmm_plan_s* p, const std::vector<int>& rp, int n_hin
   if (*std::max_element(weight.begin(), weight.end()) * P > kPanelSkewMax * total) {
     for (int r : pan_rows) {  // back to segments
       const int len = rp[r + 1] - rp[r];
-      const int s0 = rp[r] / kSplitLen;
-      for (int k = 0; k < len / kSplitLen; ++k) seg_info[(size_t)s0 + k] = make_int2(r, k);
+      const int s0 = rp[r] / kSegLen;
+      for (int k = 0; k < len / kSegLen; ++k) seg_info[(size_t)s0 + k] = make_int2(r, k);
     }
     return to_status(hipMemcpy(p->d_seg_info, seg_info.data(), seg_info.size() * sizeof(int2),
                                hipMemcpyHostToDevice));

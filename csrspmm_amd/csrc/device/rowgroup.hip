@@ -20,12 +20,12 @@
 // Load balance (large problems, "plan" mode, three launches):
 //  * plan_kernel, one thread per row, no atomics: merge-block starts and
 //    the segment slots of long rows.
-//  * rowgroup_kernel: persistent blocks walk the long-row segments (partial
+//  * rowgroup_kernel: the first blocks take the long-row segments (partial
 //    sums to the workspace); the other blocks each take one merge block of
 //    consecutive short rows and stream their contiguous nonzeros, so
 //    gathers stay in flight across row boundaries and a row's accumulator
 //    is flushed (epilogue + store) when the stream passes its end.
-//  * combine_kernel: adds each long row's partials in segment order.
+//  * combine_kernel: adds each long row's partials in a fixed order.
 // Everything is deterministic (no float atomics): results repeat bit for bit.
 
 #include "common.hpp"
@@ -36,12 +36,24 @@ namespace {
 
 constexpr int kWaves = 4;  // waves per block (256 threads)
 
+// Blocks of the combine kernel that scan the segment slots (grid-strided).
+#ifndef CSRSPMM_COMBINE_SCAN_BLOCKS
+#define CSRSPMM_COMBINE_SCAN_BLOCKS 1024
+#endif
+constexpr int kCombineScanBlocks = CSRSPMM_COMBINE_SCAN_BLOCKS;
+
 // B-row gathers in flight per lane (unroll over nonzeros) for the float4
 // single-chunk kernels; build-time tunable.
 #ifndef CSRSPMM_VEC4_UNROLL
 #define CSRSPMM_VEC4_UNROLL 4
 #endif
 constexpr int kVec4U = CSRSPMM_VEC4_UNROLL;
+
+// B-row gathers in flight per lane in the long-row segment phase, whose
+// groups each walk one long dependent chain; build-time tunable.
+#ifndef CSRSPMM_SEG_UNROLL
+#define CSRSPMM_SEG_UNROLL 4
+#endif
 
 __device__ __forceinline__ void wave_lds_sync() {
   // The LDS stage is private to the wave: order its writes against the
@@ -152,7 +164,7 @@ __device__ __forceinline__ void store_row(const Problem& p, int row, const int (
 }
 
 // Short rows [rs, re) streamed: windows of up to G consecutive rows whose
-// nonzeros form one contiguous range; a row longer than kSplitLen ends the
+// nonzeros form one contiguous range; a row longer than kLongRow ends the
 // window and is skipped (its segments are summed elsewhere).
 template <int VEC, int G, int T, int U, bool LDS>
 __device__ __forceinline__ void stream_rows(const Problem& p, const Panel<VEC, G, T>& pn, int rs,
@@ -166,7 +178,7 @@ __device__ __forceinline__ void stream_rows(const Problem& p, const Panel<VEC, G
       lo = p.rowptr[rs + gl];
       hi = p.rowptr[rs + gl + 1];
     }
-    const bool is_long = gl < nbm && (hi - lo) > kSplitLen;
+    const bool is_long = gl < nbm && (hi - lo) > kLongRow;
     const unsigned long long bl = __ballot(is_long) & gmask;
     const int nb = bl ? (__ffsll((long long)bl) - 1 - gbase) : nbm;  // rows before the first long one
     if (nb > 0) {
@@ -210,29 +222,36 @@ __global__ __launch_bounds__(kWaves * 64) void rowgroup_kernel(Problem p, int se
   int2* stage = stage_all + (LDS ? wave * 64 : 0);
 
   if ((int)blockIdx.x < seg_blocks) {
-    // Persistent phase: long-row segments, slots grid-strided.
+    // Long-row segments, one slot per group (grid-strided if the segment
+    // blocks are capped).
+    constexpr int US = CSRSPMM_SEG_UNROLL > U ? (CSRSPMM_SEG_UNROLL < G ? CSRSPMM_SEG_UNROLL : G) : U;
     for (int s = blockIdx.x * GPB + gid; s < p.nslots; s += seg_blocks * GPB) {
       const int2 si = p.seg_info[s];
       if (si.x < 0 || si.x >= p.M) continue;  // unused slot
       const int rs = p.rowptr[si.x];
       const int re = p.rowptr[si.x + 1];
-      const int nseg = (re - rs) / kSplitLen;
-      const int start = rs + si.y * kSplitLen;
-      const int end = si.y == nseg - 1 ? re : start + kSplitLen;
+      const int len = re - rs;
+      const int nseg = len / kSegLen;
+      const int start = rs + seg_begin(len, nseg, si.y);
+      const int end = rs + seg_begin(len, nseg, si.y + 1);
       float* prow = p.partials + (long long)s * p.ldp;
       for (int c0 = 0; c0 < p.N; c0 += PW) {
         const Panel<VEC, G, T> pn(p, c0, gl);
         VT acc[T];
 #pragma unroll
         for (int t = 0; t < T; ++t) acc[t] = Vec<VEC>::zero();
-        stream_nonzeros<VEC, G, T, U, LDS>(p, pn, start, end, gl, gbase, stage,
-                                           [&](int, float v, const VT(&b)[T]) {
+        stream_nonzeros<VEC, G, T, US, LDS>(p, pn, start, end, gl, gbase, stage,
+                                            [&](int, float v, const VT(&b)[T]) {
 #pragma unroll
-                                             for (int t = 0; t < T; ++t) acc[t] = fma_v(v, b[t], acc[t]);
-                                           });
+                                              for (int t = 0; t < T; ++t) acc[t] = fma_v(v, b[t], acc[t]);
+                                            });
+        if (nseg == 1) {  // the whole row: epilogue and store here
+          store_row<VEC, T>(p, si.x, pn.col, pn.cval, acc);
+        } else {
 #pragma unroll
-        for (int t = 0; t < T; ++t) {
-          if (pn.cval[t]) *reinterpret_cast<VT*>(prow + pn.col[t]) = acc[t];
+          for (int t = 0; t < T; ++t) {
+            if (pn.cval[t]) *reinterpret_cast<VT*>(prow + pn.col[t]) = acc[t];
+          }
         }
       }
     }
@@ -292,94 +311,142 @@ __global__ __launch_bounds__(256) void plan_kernel(Problem p) {
     }
     // slots [x0 / S, x1 / S) belong to row r; a long row uses the first nseg
     const int x1 = clamp_nnz(p.rowptr[r + 1], p.nnz);
-    const int s0 = x0 / kSplitLen;
-    const int s1 = min(max(s0, x1 / kSplitLen), p.nslots);
+    const int s0 = x0 / kSegLen;
+    const int s1 = min(max(s0, x1 / kSegLen), p.nslots);
     const int len = x1 - x0;
-    const int nseg = len > kSplitLen ? len / kSplitLen : 0;
+    const int nseg = len > kLongRow ? len / kSegLen : 0;
     for (int s = s0; s < s1; ++s)
       p.seg_info[s] = (s - s0) < nseg ? make_int2(r, s - s0) : make_int2(-1, 0);
   }
 }
 
-// One wave per long row (found at its first slot): C[row] = epilogue(sum of
-// the row's segment partials).  The wave is split into P = 64 / GC lane
-// groups (GC lanes cover a column panel); group q sums segments q, q+P, ...
-// in order, then the P group sums are added by a fixed xor-shuffle tree, so
-// the result does not depend on timing.
+// Partials k = q, q + NG, q + 2*NG, ... (k < n) of one lane's columns, added
+// in that order; partial k sits at src + idx(k) * ldp, idx(k) = pieces[k]
+// when a piece list is given, else k.
+template <int VEC, int NG>
+__device__ __forceinline__ typename Vec<VEC>::T sum_strided(const float* src, const int* pieces,
+                                                            int n, int q, long long ldp, bool cv) {
+  using VT = typename Vec<VEC>::T;
+  VT acc = Vec<VEC>::zero();
+  if (!cv) return acc;
+  auto part = [&](int k) -> VT {
+    const long long idx = pieces ? (long long)pieces[k] : (long long)k;
+    return *reinterpret_cast<const VT*>(src + idx * ldp);
+  };
+  int k = q;
+  for (; k + 7 * NG < n; k += 8 * NG) {
+    VT a[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) a[u] = part(k + u * NG);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc = add_v(acc, a[u]);
+  }
+  for (; k < n; k += NG) acc = add_v(acc, part(k));
+  return acc;
+}
+
+// Sum over the 64 / GC lane groups of a wave by a fixed xor-shuffle tree;
+// every group ends with the total.
+template <int GC>
+__device__ __forceinline__ float wave_group_sum(float v) {
+#pragma unroll
+  for (int off = GC; off < 64; off <<= 1) v += __shfl_xor(v, off);
+  return v;
+}
+template <int GC>
+__device__ __forceinline__ f4 wave_group_sum(f4 v) {
+#pragma unroll
+  for (int off = GC; off < 64; off <<= 1) {
+    v.x += __shfl_xor(v.x, off);
+    v.y += __shfl_xor(v.y, off);
+    v.z += __shfl_xor(v.z, off);
+    v.w += __shfl_xor(v.w, off);
+  }
+  return v;
+}
+
+// C rows of split long rows (one partial per segment) and of panelized rows
+// (one partial per piece), each the sum of its partials in a fixed order, so
+// results repeat bit for bit.  A wave's lanes form P = 64 / GC groups of GC
+// lanes, each group covering GC * VEC columns.
+//  * Blocks [0, scan_blocks): a wave reads 64 consecutive segment slots at
+//    once, finds by ballot the rows whose first segment lies among them, and
+//    sums the segments of each such row that has two or more: group q takes segments q, q + P, ..., then
+//    the P group sums meet in the xor tree.
+//  * Blocks [scan_blocks, ...): one panelized row per block.  Its 4 waves'
+//    4P groups split the pieces the same way; each wave's sum goes to LDS and
+//    wave 0 adds the four in wave order.
 template <int VEC, int GC>
-__global__ __launch_bounds__(256) void combine_kernel(Problem p) {
+__global__ __launch_bounds__(kWaves * 64) void combine_kernel(Problem p, int scan_blocks) {
   using VT = typename Vec<VEC>::T;
   constexpr int P = 64 / GC;
   const int lane = lane_id();
   const int q = lane / GC;
   const int gl = lane & (GC - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int nw = blockDim.x >> 6;
-  for (int s = blockIdx.x * nw + wave; s < p.nslots + p.npan; s += gridDim.x * nw) {
-    int row, nseg;
-    const float* base;
-    const int* pieces = nullptr;  // panelized row: partial index of each piece
-    if (s < p.nslots) {  // a split long row, found at its first slot
-      const int2 si = p.seg_info[s];
-      if (si.x < 0 || si.x >= p.M || si.y != 0) continue;
-      row = si.x;
-      nseg = (p.rowptr[row + 1] - p.rowptr[row]) / kSplitLen;
-      base = p.partials + (long long)s * p.ldp;
-    } else {  // a panelized row of a stored plan
-      const int i = s - p.nslots;
-      row = p.pan_rows[i];
-      nseg = p.pan_ptr[i + 1] - p.pan_ptr[i];
-      base = p.pan_part;
-      pieces = p.pan_piece + p.pan_ptr[i];
-    }
-    float* crow = p.C + (long long)row * p.ldc;
-    for (int c0 = 0; c0 < p.N; c0 += GC * VEC) {
-      const int c = c0 + gl * VEC;
-      const bool cv = c < p.N;
-      const float* src = base + c;
-      // partial k of this row
-      auto part = [&](int k) -> VT {
-        const long long idx = pieces ? (long long)pieces[k] : (long long)k;
-        return *reinterpret_cast<const VT*>(src + idx * p.ldp);
-      };
-      VT acc = Vec<VEC>::zero();
-      int k = q;
-      for (; k + 3 * P < nseg; k += 4 * P) {
-        VT a[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) a[u] = cv ? part(k + u * P) : Vec<VEC>::zero();
-#pragma unroll
-        for (int u = 0; u < 4; ++u) acc = add_v(acc, a[u]);
-      }
-      for (; k < nseg; k += P)
-        if (cv) acc = add_v(acc, part(k));
-#pragma unroll
-      for (int off = GC; off < 64; off <<= 1) {
-        if constexpr (VEC == 1) {
-          acc += __shfl_xor(acc, off);
-        } else {
-          acc.x += __shfl_xor(acc.x, off);
-          acc.y += __shfl_xor(acc.y, off);
-          acc.z += __shfl_xor(acc.z, off);
-          acc.w += __shfl_xor(acc.w, off);
+  if ((int)blockIdx.x < scan_blocks) {
+    const int nchunks = div_up(p.nslots, 64);
+    for (int ch = blockIdx.x * kWaves + wave; ch < nchunks; ch += scan_blocks * kWaves) {
+      const int s = ch * 64 + lane;
+      int2 si = make_int2(-1, 1);
+      if (s < p.nslots) si = p.seg_info[s];
+      unsigned long long firsts = __ballot(si.x >= 0 && si.x < p.M && si.y == 0);
+      while (firsts) {
+        const int l = __ffsll((long long)firsts) - 1;
+        firsts &= firsts - 1;
+        const int row = __builtin_amdgcn_readlane(si.x, l);
+        const int nseg = (p.rowptr[row + 1] - p.rowptr[row]) / kSegLen;
+        if (nseg < 2) continue;  // stored by the segment phase
+        const float* base = p.partials + (long long)(ch * 64 + l) * p.ldp;
+        float* crow = p.C + (long long)row * p.ldc;
+        for (int c0 = 0; c0 < p.N; c0 += GC * VEC) {
+          const int c = c0 + gl * VEC;
+          const bool cv = c < p.N;
+          const VT acc = wave_group_sum<GC>(sum_strided<VEC, P>(base + c, nullptr, nseg, q, p.ldp, cv));
+          if (q == 0 && cv) store_epi<VEC>(p, crow + c, acc);
         }
       }
-      if (q == 0 && cv) store_epi<VEC>(p, crow + c, acc);
     }
+    return;
+  }
+  const int i = (int)blockIdx.x - scan_blocks;
+  if (i >= p.npan) return;
+  __shared__ VT wave_sum[kWaves][GC];
+  const int row = p.pan_rows[i];
+  const int npc = p.pan_ptr[i + 1] - p.pan_ptr[i];
+  const int* pieces = p.pan_piece + p.pan_ptr[i];
+  float* crow = p.C + (long long)row * p.ldc;
+  for (int c0 = 0; c0 < p.N; c0 += GC * VEC) {
+    const int c = c0 + gl * VEC;
+    const bool cv = c < p.N;
+    const VT acc = wave_group_sum<GC>(
+        sum_strided<VEC, kWaves * P>(p.pan_part + c, pieces, npc, wave * P + q, p.ldp, cv));
+    if (q == 0) wave_sum[wave][gl] = acc;
+    __syncthreads();
+    if (wave == 0 && q == 0 && cv) {
+      VT t = wave_sum[0][gl];
+#pragma unroll
+      for (int w = 1; w < kWaves; ++w) t = add_v(t, wave_sum[w][gl]);
+      store_epi<VEC>(p, crow + c, t);
+    }
+    __syncthreads();
   }
 }
 
 template <int VEC>
-void launch_combine(const Problem& p, int blocks, hipStream_t s) {
+void launch_combine(const Problem& p, hipStream_t s) {
   const int chunks = (p.N + VEC - 1) / VEC;
+  const int scan_blocks = std::min(kCombineScanBlocks, div_up_host(div_up_host(p.nslots, 64), kWaves));
+  const int blocks = scan_blocks + p.npan;
+  if (blocks == 0) return;
   if (chunks <= 8) {
-    hipLaunchKernelGGL((combine_kernel<VEC, 8>), dim3(blocks), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((combine_kernel<VEC, 8>), dim3(blocks), dim3(kWaves * 64), 0, s, p, scan_blocks);
   } else if (chunks <= 16) {
-    hipLaunchKernelGGL((combine_kernel<VEC, 16>), dim3(blocks), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((combine_kernel<VEC, 16>), dim3(blocks), dim3(kWaves * 64), 0, s, p, scan_blocks);
   } else if (chunks <= 32) {
-    hipLaunchKernelGGL((combine_kernel<VEC, 32>), dim3(blocks), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((combine_kernel<VEC, 32>), dim3(blocks), dim3(kWaves * 64), 0, s, p, scan_blocks);
   } else {
-    hipLaunchKernelGGL((combine_kernel<VEC, 64>), dim3(blocks), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((combine_kernel<VEC, 64>), dim3(blocks), dim3(kWaves * 64), 0, s, p, scan_blocks);
   }
 }
 
@@ -389,7 +456,7 @@ hipError_t launch_rg(const Problem& p, hipStream_t s) {
   const int units = p.plan ? p.nblocks : p.M;
   const int unit_blocks = div_up_host(units, GPB);
   const int seg_blocks =
-      (p.plan && p.nslots > 0) ? std::min(kPersistentBlocks, div_up_host(p.nslots, GPB)) : 0;
+      (p.plan && p.nslots > 0) ? std::min(kSegBlocksMax, div_up_host(p.nslots, GPB)) : 0;
   const long long blocks = (long long)unit_blocks + seg_blocks;
   if (blocks == 0) return hipSuccess;
   timing_before_main(s);
@@ -459,11 +526,10 @@ hipError_t launch_rowgroup(const Problem& p, int vec, bool lds, hipStream_t s) {
   }
   if (e != hipSuccess) return e;
   if (p.plan && p.nslots + p.npan > 0) {
-    const int cblocks = std::min(kPersistentBlocks, div_up_host(p.nslots + p.npan, 4));
     if (vec == 4) {
-      launch_combine<4>(p, cblocks, s);
+      launch_combine<4>(p, s);
     } else {
-      launch_combine<1>(p, cblocks, s);
+      launch_combine<1>(p, s);
     }
     e = hipGetLastError();
   }

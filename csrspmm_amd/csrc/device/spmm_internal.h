@@ -18,22 +18,34 @@ enum EpilogueMode : int {
                        // it (the torch forwards' zeros()+beta, torch_csrspmm_naive.cpp:32-34)
 };
 
-// Long rows.  A row of len > kSplitLen nonzeros is cut into
-// floor(len / kSplitLen) segments: segment k covers nonzeros
-// [k*kSplitLen, (k+1)*kSplitLen) of the row and the last segment also takes
-// the remainder (so segments hold kSplitLen..2*kSplitLen-1 nonzeros).  Each
-// segment's partial sum goes to a workspace slot; a combine pass adds the
-// partials of a row in segment order and applies the epilogue.
+// Long rows.  A row of len > kLongRow nonzeros is cut into
+// nseg = floor(len / kSegLen) segments of near-equal length: segment k covers
+// nonzeros [seg_begin(len, nseg, k), seg_begin(len, nseg, k + 1)) of the row,
+// so a row's segments differ in length by at most one (kSegLen..2*kSegLen-1
+// nonzeros for a single segment, at most (3/2)*kSegLen from two on).  A row
+// with one segment is summed whole and stored with the epilogue directly;
+// otherwise each segment's partial sum goes to a workspace slot and a
+// combine pass adds the partials of the row in segment order and applies the
+// epilogue.
 //
 // Slot ownership needs no counters: row r owns slots
-// [rowptr[r] / kSplitLen, rowptr[r+1] / kSplitLen), a range at least as long
-// as its segment count, and the ranges of all rows tile [0, nnz / kSplitLen).
-#ifndef CSRSPMM_SPLIT_LEN
-#define CSRSPMM_SPLIT_LEN 256
+// [rowptr[r] / kSegLen, rowptr[r+1] / kSegLen), a range at least as long
+// as its segment count, and the ranges of all rows tile [0, nnz / kSegLen).
+#ifndef CSRSPMM_SEG_LEN
+#define CSRSPMM_SEG_LEN 256
 #endif
-constexpr int kSplitLen = CSRSPMM_SPLIT_LEN;
+#ifndef CSRSPMM_LONG_ROW
+#define CSRSPMM_LONG_ROW 256
+#endif
+constexpr int kSegLen = CSRSPMM_SEG_LEN;
+constexpr int kLongRow = CSRSPMM_LONG_ROW;
+static_assert(kLongRow >= kSegLen, "a long row needs at least one segment");
 
-// Short rows (len <= kSplitLen) are streamed in merge-path blocks: with the
+__host__ __device__ inline int seg_begin(int len, int nseg, int k) {
+  return static_cast<int>((static_cast<long long>(k) * len) / nseg);
+}
+
+// Short rows (len <= kLongRow) are streamed in merge-path blocks: with the
 // strictly increasing merge coordinate F(r) = r + rowptr[r], block b holds
 // the rows r with F(r) in [b*kMergeBlock, (b+1)*kMergeBlock), so every block
 // carries at most kMergeBlock (rows + nonzeros) of short-row work plus one
@@ -51,11 +63,13 @@ constexpr long long kPlanMinItems = 1 << 16;
 // workgroup id, which stored plans use for L2 locality (plan.hip).
 constexpr int kXcds = 8;
 
-// Blocks of the persistent segment phase / combine phase: a few per CU.
-#ifndef CSRSPMM_PERSISTENT_BLOCKS
-#define CSRSPMM_PERSISTENT_BLOCKS 1024
+// Cap on the blocks of the segment phase.  By default every segment slot
+// gets its own group, so the hardware dispatcher balances segments across
+// CUs; a smaller cap makes the segment blocks persistent (grid-strided).
+#ifndef CSRSPMM_SEG_BLOCKS_MAX
+#define CSRSPMM_SEG_BLOCKS_MAX (1 << 24)
 #endif
-constexpr int kPersistentBlocks = CSRSPMM_PERSISTENT_BLOCKS;
+constexpr int kSegBlocksMax = CSRSPMM_SEG_BLOCKS_MAX;
 
 struct Problem {
   int M, K, N, nnz;
@@ -71,7 +85,7 @@ struct Problem {
   // Plan (all inside the workspace, all written by plan_kernel each call).
   // plan == false: every row is processed whole by its own group.
   bool plan;
-  int nslots;         // nnz / kSplitLen
+  int nslots;         // nnz / kSegLen
   int nblocks;        // merge blocks
   int* block_start;   // nblocks + 1 entries: first row of each merge block, then M
   int2* seg_info;     // per slot: (row, segment index) or (-1, 0) for an unused slot

@@ -6,6 +6,11 @@ FETCH_SIZE / WRITE_SIZE readings calibrate the counters.
         --config xl --algo WarpPerRowFp4 --calls 20
     rocprofv3 --pmc FETCH_SIZE -d OUT -- python3 -m csrspmm_amd.profile_run \
         --config xl --algo WarpPerRowFp4 --calls 3 --copy-mib 1024
+    rocprofv3 --kernel-trace --stats -d OUT -- python3 -m csrspmm_amd.profile_run \
+        --config xl --algo Auto --plan --calls 20
+
+With --plan the calls go through one stored plan (csrspmm_plan_*) built
+before the first call.
 """
 from __future__ import annotations
 
@@ -19,6 +24,7 @@ def main(argv=None):
     ap.add_argument("--config", default="xl")
     ap.add_argument("--algo", default="WarpPerRowFp4")
     ap.add_argument("--calls", type=int, default=20)
+    ap.add_argument("--plan", action="store_true", help="call through a stored plan")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run one device-to-device copy of this many MiB")
     args = ap.parse_args(argv)
@@ -45,11 +51,22 @@ def main(argv=None):
         torch.cuda.synchronize()
         print(f"[profile_run] copy of {args.copy_mib} MiB done", flush=True)
         del src, dst
+    plan = None
+    if args.plan:
+        plan = capi.Plan(args.algo, rp, ci, va, a.K, n_hint=cfg.N)
+        torch.cuda.synchronize()
+        print(f"[profile_run] plan {plan.algorithm}: {plan.panelized_rows} panelized rows, "
+              f"{plan.device_bytes} device bytes", flush=True)
     t0 = time.perf_counter()
     for i in range(args.calls):
-        capi.spmm(args.algo, rp, ci, va, dB, C, 1.0, 0.0)
+        if plan is not None:
+            plan.spmm(dB, C, 1.0, 0.0)
+        else:
+            capi.spmm(args.algo, rp, ci, va, dB, C, 1.0, 0.0)
     torch.cuda.synchronize()
     print(f"[profile_run] {args.calls} calls in {time.perf_counter() - t0:.3f}s", flush=True)
+    if plan is not None:
+        plan.close()
     return 0
 
 
