@@ -1,12 +1,13 @@
 """Benchmark: CSR SpMM on one MI355X, C = A*B (alpha=1, beta=0).
 
-    python bench.py [--steps K] [--warmup W] [--config xl] [--algo WarpPerRowFp4]
+    python bench.py [--steps K] [--warmup W] [--config xl] [--algo Auto]
 
 A step is one SpMM call (all its launches) over the named config with every
 input already resident in HBM.  W untimed steps, then K timed steps between
 two torch.cuda.synchronize() calls, timed with HIP events on the launch
 stream.  Prints ONE JSON line:
   value      GFLOPS = 2*nnz*N / (ms_per_step) for the headline variant
+             (Auto by default: the variant the library picks from N)
   roofline   achieved gather-model GB/s of the main kernel (HIP event pair
              around it, csrspmm_timing_*) against 8 TB/s
   variants   the same figures for every variant on the same config
@@ -41,7 +42,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="xl")
-    ap.add_argument("--algo", default="WarpPerRowFp4")
+    ap.add_argument("--algo", default="Auto")
     ap.add_argument("--variants", default="all", help="'all', 'none' or comma list")
     ap.add_argument("--variant-steps", type=int, default=20)
     ap.add_argument("--plan-algo", default="Auto", help="stored-plan leg ('none' disables it)")
@@ -175,15 +176,18 @@ def main():
             "frac": round(balg / (main_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         }
 
+    lib = capi.hip()
+    resolved = lib.csrspmm_algorithm_name(
+        lib.csrspmm_resolve_algorithm(capi.ALGO[args.algo], N)).decode()
     ms, main_ms = time_variant(capi, torch, args.algo, d, args.steps, args.warmup)
-    print(f"[bench] {args.algo}: {ms:.4f} ms/call, main kernel {main_ms:.4f} ms",
+    print(f"[bench] {args.algo} ({resolved}): {ms:.4f} ms/call, main kernel {main_ms:.4f} ms",
           file=sys.stderr, flush=True)
 
     variants = {}
     if args.variants != "none":
         names = ALGORITHMS if args.variants == "all" else args.variants.split(",")
         for name in names:
-            if name == args.algo:
+            if name == resolved:
                 variants[name] = figures(ms, main_ms)
                 continue
             vms, vmain = time_variant(capi, torch, name, d, args.variant_steps, 3)
@@ -205,7 +209,7 @@ def main():
     if os.path.exists(args.traffic_file):
         with open(args.traffic_file) as f:
             tr = json.load(f)
-        key = f"{cfg.name}/{args.algo}"
+        key = f"{cfg.name}/{resolved}"
         if key in tr:
             traffic = tr[key]["bytes_per_launch"]
 
@@ -229,11 +233,12 @@ def main():
         "dtype": "f32",
         "data": "synthetic (seeded generator, csrspmm_amd/configs.py)",
         "config": {"workload": cfg.name, "description": cfg.description, "algo": args.algo,
+                   "resolved_algo": resolved,
                    "M": a.M, "K": a.K, "N": N, "nnz": a.nnz, "max_row_nnz": a.max_row_nnz,
                    "alpha": 1.0, "beta": 0.0, "bytes_alg": balg},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "kernel": f"{args.algo} main kernel",
+                     "traffic": traffic, "kernel": f"{resolved} main kernel",
                      "kernel_ms": round(main_ms, 5)},
         "cpu_baseline": cpu,
         "variants": variants,
