@@ -24,7 +24,8 @@ CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "lib")
 INC = os.path.join(ROOT, "include")
 
-HIP_SOURCES = ["device/capi.hip", "device/rowgroup.hip", "device/naive.hip", "device/plan.hip"]
+HIP_SOURCES = ["device/capi.hip", "device/rowgroup.hip", "device/naive.hip", "device/plan.hip",
+               "device/csr_tools.hip"]
 HOST_SOURCES = ["host/csrspmm.cpp", "host/spmm_launcher.cpp", "host/csr_utils.cpp",
                 "host/dense_utils.cpp", "host/gen.cpp"]
 

@@ -46,6 +46,12 @@ HIP_API = {
     "csrspmm_plan_destroy": (_c_int, [_c_void_p]),
     "csrspmm_validate_csr": (_c_int, [_c_int, _c_int, _c_int, _c_void_p, _c_void_p,
                                       ctypes.POINTER(_c_int), ctypes.POINTER(_c_int), _c_void_p]),
+    "csrspmm_dense2csr_count_f32": (_c_int, [_c_int, _c_int, _c_void_p, _c_ll, _c_float, _c_void_p,
+                                             _c_void_p, _c_void_p]),
+    "csrspmm_dense2csr_fill_f32": (_c_int, [_c_int, _c_int, _c_void_p, _c_ll, _c_float, _c_void_p,
+                                            _c_void_p, _c_void_p, _c_void_p]),
+    "csrspmm_csr_max_row_nnz": (_c_int, [_c_int, _c_void_p, _c_void_p, _c_void_p]),
+    "csrspmm_indices_i64_to_i32": (_c_int, [_c_void_p, _c_void_p, _c_ll, _c_void_p, _c_void_p]),
     "csrspmm_device_malloc": (_c_int, [ctypes.POINTER(_c_void_p), _c_size_t]),
     "csrspmm_device_free": (_c_int, [_c_void_p]),
     "csrspmm_memcpy_h2d": (_c_int, [_c_void_p, _c_void_p, _c_size_t]),
@@ -233,3 +239,45 @@ def validate(rowptr, colidx, K, stream=None):
                                      ctypes.byref(f), ctypes.byref(m), ctypes.c_void_p(stream)),
           "csrspmm_validate_csr")
     return f.value, m.value
+
+
+def _stream_of(t, stream):
+    return torch.cuda.current_stream(t.device).cuda_stream if stream is None else stream
+
+
+def dense2csr(D, tol=0.0, stream=None):
+    """Device dense -> CSR (rowptr, colidx, vals); one host sync to size the
+    arrays."""
+    M, K = D.shape
+    s = _stream_of(D, stream)
+    rowptr = torch.empty(M + 1, dtype=torch.int32, device=D.device)
+    nnz = torch.empty(1, dtype=torch.int64, device=D.device)
+    ld = D.stride(0) if M > 0 and K > 1 else max(K, 1)
+    check(hip().csrspmm_dense2csr_count_f32(M, K, _ptr(D), ld, tol, _ptr(rowptr), _ptr(nnz),
+                                            ctypes.c_void_p(s)), "csrspmm_dense2csr_count_f32")
+    n = int(nnz.item())
+    colidx = torch.empty(n, dtype=torch.int32, device=D.device)
+    vals = torch.empty(n, dtype=torch.float32, device=D.device)
+    check(hip().csrspmm_dense2csr_fill_f32(M, K, _ptr(D), ld, tol, _ptr(rowptr), _ptr(colidx),
+                                           _ptr(vals), ctypes.c_void_p(s)),
+          "csrspmm_dense2csr_fill_f32")
+    return rowptr, colidx, vals
+
+
+def max_row_nnz(rowptr, stream=None):
+    """Longest row, as a one-element int32 device tensor (no host sync)."""
+    out = torch.empty(1, dtype=torch.int32, device=rowptr.device)
+    check(hip().csrspmm_csr_max_row_nnz(rowptr.numel() - 1, _ptr(rowptr), _ptr(out),
+                                        ctypes.c_void_p(_stream_of(rowptr, stream))),
+          "csrspmm_csr_max_row_nnz")
+    return out
+
+
+def narrow_indices(idx64, stream=None):
+    """(int32 copy, one-element int32 overflow flag), both on the device."""
+    dst = torch.empty(idx64.numel(), dtype=torch.int32, device=idx64.device)
+    flag = torch.empty(1, dtype=torch.int32, device=idx64.device)
+    check(hip().csrspmm_indices_i64_to_i32(_ptr(idx64), _ptr(dst), idx64.numel(), _ptr(flag),
+                                           ctypes.c_void_p(_stream_of(idx64, stream))),
+          "csrspmm_indices_i64_to_i32")
+    return dst, flag

@@ -92,6 +92,25 @@ int main(int argc, char** argv) {
         csrspmm::dense_free_device(dB);
         csrspmm::dense_free_device(dC);
     }
+    if (algo_str == "all") {
+        // the device dense -> CSR must give the host dense2csr's arrays exactly
+        csrspmm::DenseMatrix dDense;
+        csrspmm::dense_host2device(hA, dDense);
+        csrspmm::CSRMatrix dA2, hA2;
+        csrspmm::dense2csr_device(dDense, dA2, 0.0f);
+        csrspmm::csr_device2host(dA2, hA2);
+        const bool same =
+            hA2.nnz == hA_csr.nnz && hA2.max_row_nnz == hA_csr.max_row_nnz &&
+            std::memcmp(hA2.row_ptr, hA_csr.row_ptr, sizeof(int) * ((size_t)M + 1)) == 0 &&
+            std::memcmp(hA2.col_idx, hA_csr.col_idx, sizeof(int) * (size_t)hA_csr.nnz) == 0 &&
+            std::memcmp(hA2.values, hA_csr.values, sizeof(float) * (size_t)hA_csr.nnz) == 0;
+        std::cout << (same ? "Pass: " : "Error: ") << "dense2csr_device nnz=" << hA2.nnz
+                  << " max_row_nnz=" << hA2.max_row_nnz << std::endl;
+        failures += same ? 0 : 1;
+        csrspmm::csr_free_host(hA2);
+        csrspmm::csr_free_device(dA2);
+        csrspmm::dense_free_device(dDense);
+    }
     csrspmm::dense_free_host(hA);
     csrspmm::dense_free_host(hB);
     csrspmm::dense_free_host(hC);

@@ -98,6 +98,38 @@ void dense2csr(const DenseMatrix& dense, CSRMatrix& csr, float tol) {
     csr.max_row_nnz = mx;
 }
 
+void dense2csr_device(const DenseMatrix& d_dense, CSRMatrix& d_csr, float tol) {
+    if (!d_dense.data || d_dense.height <= 0 || d_dense.width <= 0)
+        die("dense2csr_device: invalid dense matrix");
+    if (d_csr.row_ptr || d_csr.col_idx || d_csr.values)
+        die("dense2csr_device error: destination must be null.");
+    const int H = d_dense.height, W = d_dense.width;
+    int* rowptr = nullptr;
+    long long* d_nnz = nullptr;
+    int* d_max = nullptr;
+    csrspmmCheck(csrspmm_device_malloc(reinterpret_cast<void**>(&rowptr), ((size_t)H + 1) * sizeof(int)));
+    csrspmmCheck(csrspmm_device_malloc(reinterpret_cast<void**>(&d_nnz), sizeof(long long)));
+    csrspmmCheck(csrspmm_device_malloc(reinterpret_cast<void**>(&d_max), sizeof(int)));
+    csrspmmCheck(csrspmm_dense2csr_count_f32(H, W, d_dense.data, W, tol, rowptr, d_nnz, nullptr));
+    long long nnz = 0;
+    csrspmmCheck(csrspmm_memcpy_d2h(&nnz, d_nnz, sizeof(nnz)));
+    if (nnz > 0x7fffffffLL) die("dense2csr_device: nnz exceeds int32");
+    d_csr.height = H;
+    d_csr.width = W;
+    d_csr.nnz = (int)nnz;
+    d_csr.row_ptr = rowptr;
+    csrspmmCheck(csrspmm_device_malloc(reinterpret_cast<void**>(&d_csr.col_idx),
+                                       std::max<size_t>((size_t)nnz, 1) * sizeof(int)));
+    csrspmmCheck(csrspmm_device_malloc(reinterpret_cast<void**>(&d_csr.values),
+                                       std::max<size_t>((size_t)nnz, 1) * sizeof(float)));
+    csrspmmCheck(csrspmm_dense2csr_fill_f32(H, W, d_dense.data, W, tol, rowptr, d_csr.col_idx,
+                                            d_csr.values, nullptr));
+    csrspmmCheck(csrspmm_csr_max_row_nnz(H, rowptr, d_max, nullptr));
+    csrspmmCheck(csrspmm_memcpy_d2h(&d_csr.max_row_nnz, d_max, sizeof(int)));
+    csrspmmCheck(csrspmm_device_free(d_nnz));
+    csrspmmCheck(csrspmm_device_free(d_max));
+}
+
 void csr2dense(const CSRMatrix& csr, DenseMatrix& dense) {
     if (!csr.row_ptr || !csr.col_idx || !csr.values || csr.height <= 0 || csr.width <= 0)
         die("csr2dense: invalid csr");

@@ -13,6 +13,8 @@
 // default stream, shapes / contiguity are checked, and a failed launch raises.
 #include <torch/extension.h>
 
+#include <vector>
+
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 
@@ -235,9 +237,83 @@ class CsrSpmmPlan {
   csrspmm_plan_t plan_ = nullptr;
 };
 
+// The forwards' semantics (new C, beta scaling zero) for a named variant.
+Tensor csrspmm_forward_named(Tensor A_row_ptr, Tensor A_col_idx, Tensor A_values, Tensor B,
+                             double alpha, double beta, const std::string& algo) {
+  return forward(algo_id(algo), A_row_ptr, A_col_idx, A_values, -1, B, alpha, beta);
+}
+
+hipStream_t stream_of(const Tensor& t) {
+  return c10::hip::getCurrentHIPStream(t.device().index()).stream();
+}
+
+// Device dense -> CSR: (rowptr, colidx, values).  One host sync, to size
+// colidx/values from the count.
+std::vector<Tensor> dense_to_csr(Tensor D, double tol) {
+  TORCH_CHECK(D.is_cuda(), "dense must be a CUDA tensor");
+  TORCH_CHECK(D.dtype() == torch::kFloat32, "dense must be float32");
+  TORCH_CHECK(D.dim() == 2, "dense must be 2-D");
+  TORCH_CHECK(D.size(1) <= 1 || D.stride(1) == 1, "dense must be row-major (stride(1) == 1)");
+  TORCH_CHECK(D.size(0) < INT32_MAX && D.size(1) <= INT32_MAX, "sizes must fit int32");
+  c10::DeviceGuard guard(D.device());
+  const int M = static_cast<int>(D.size(0)), K = static_cast<int>(D.size(1));
+  const long long ld = K <= 1 ? std::max(K, 1) : D.stride(0);
+  Tensor rowptr = torch::empty({M + 1}, D.options().dtype(torch::kInt32));
+  Tensor nnz = torch::empty({1}, D.options().dtype(torch::kInt64));
+  hipStream_t s = stream_of(D);
+  const float* d = D.numel() ? D.data_ptr<float>() : nullptr;
+  int st = csrspmm_dense2csr_count_f32(M, K, d, ld, static_cast<float>(tol), rowptr.data_ptr<int>(),
+                                       reinterpret_cast<long long*>(nnz.data_ptr<int64_t>()), s);
+  TORCH_CHECK(st == 0, "dense_to_csr failed: ", csrspmm_status_string(st));
+  const int64_t n = nnz.item<int64_t>();
+  TORCH_CHECK(n <= INT32_MAX, "dense_to_csr: ", n, " nonzeros exceed int32");
+  Tensor colidx = torch::empty({n}, D.options().dtype(torch::kInt32));
+  Tensor vals = torch::empty({n}, D.options());
+  st = csrspmm_dense2csr_fill_f32(M, K, d, ld, static_cast<float>(tol), rowptr.data_ptr<int>(),
+                                  n ? colidx.data_ptr<int>() : nullptr,
+                                  n ? vals.data_ptr<float>() : nullptr, s);
+  TORCH_CHECK(st == 0, "dense_to_csr failed: ", csrspmm_status_string(st));
+  return {rowptr, colidx, vals};
+}
+
+// Longest row as a one-element int32 CUDA tensor, with no host sync.
+Tensor csr_max_row_nnz(Tensor rowptr) {
+  TORCH_CHECK(rowptr.is_cuda() && rowptr.dtype() == torch::kInt32 && rowptr.dim() == 1 &&
+                  rowptr.size(0) >= 1 && rowptr.is_contiguous(),
+              "rowptr must be a contiguous 1-D int32 CUDA tensor");
+  c10::DeviceGuard guard(rowptr.device());
+  Tensor out = torch::empty({1}, rowptr.options());
+  const int st = csrspmm_csr_max_row_nnz(static_cast<int>(rowptr.size(0) - 1),
+                                         rowptr.data_ptr<int>(), out.data_ptr<int>(),
+                                         stream_of(rowptr));
+  TORCH_CHECK(st == 0, "csr_max_row_nnz failed: ", csrspmm_status_string(st));
+  return out;
+}
+
+// int64 -> int32 CSR indices on the device; int32 input is returned as is.
+// Values beyond int32 are not checked here (no sync); callers that know
+// nnz and K fit int32 need no check for a valid CSR.
+Tensor indices_to_int32(Tensor idx) {
+  TORCH_CHECK(idx.is_cuda() && idx.dim() == 1, "indices must be a 1-D CUDA tensor");
+  if (idx.dtype() == torch::kInt32) return idx.contiguous();
+  TORCH_CHECK(idx.dtype() == torch::kInt64, "indices must be int32 or int64");
+  c10::DeviceGuard guard(idx.device());
+  Tensor src = idx.contiguous();
+  Tensor dst = torch::empty({src.size(0)}, src.options().dtype(torch::kInt32));
+  const int st = csrspmm_indices_i64_to_i32(
+      reinterpret_cast<const long long*>(src.numel() ? src.data_ptr<int64_t>() : nullptr),
+      src.numel() ? dst.data_ptr<int>() : nullptr, src.numel(), nullptr, stream_of(src));
+  TORCH_CHECK(st == 0, "indices_to_int32 failed: ", csrspmm_status_string(st));
+  return dst;
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.def("csrspmm_forward", &csrspmm_forward_named, "CSR SpMM by variant name (new C)");
+  m.def("dense_to_csr", &dense_to_csr, "device dense -> CSR (rowptr, colidx, values)");
+  m.def("csr_max_row_nnz", &csr_max_row_nnz, "longest row, on the device");
+  m.def("indices_to_int32", &indices_to_int32, "int64 -> int32 CSR indices, on the device");
   m.def("csrspmm_auto", &csrspmm_auto_forward, "CSR SpMM (variant picked from N)");
   m.def("csrspmm_spmm_out", &csrspmm_spmm_out, "CSR SpMM into C in place (C = alpha*A*B + beta*C)");
   pybind11::class_<CsrSpmmPlan>(m, "CsrSpmmPlan")

@@ -27,8 +27,10 @@ __all__ = [
     "csrspmm_warp_per_row_smem_fp4",
 ]
 # Beyond the reference's five: the variant picked from N, an in-place product
-# with a real beta, and a stored plan for repeated products with one A.
-EXTRAS = ["csrspmm_auto", "csrspmm_spmm_out", "CsrSpmmPlan"]
+# with a real beta, a stored plan for repeated products with one A, and
+# device-side CSR tooling (torch.sparse_csr input, dense -> CSR, longest row).
+EXTRAS = ["csrspmm_auto", "csrspmm_spmm_out", "CsrSpmmPlan", "csrspmm_sparse", "from_sparse_csr",
+          "dense_to_csr", "csr_max_row_nnz"]
 
 
 def csrspmm_naive(A_rowptr, A_colidx, A_values, B, alpha, beta):
@@ -93,3 +95,45 @@ class CsrSpmmPlan:
     @property
     def panelized_rows(self):
         return self._plan.panelized_rows
+
+
+def from_sparse_csr(A):
+    """(rowptr, colidx, values, K) of a torch.sparse_csr CUDA tensor, ready for
+    the entry points, with no host sync: int32 indices are used in place
+    (zero-copy) and int64 indices are narrowed on the device.  A's shapes
+    must fit int32, which makes the narrowing exact for a valid CSR."""
+    if A.layout != torch.sparse_csr:
+        raise RuntimeError("A must be a torch.sparse_csr tensor")
+    if not A.is_cuda:
+        raise RuntimeError("A must be a CUDA tensor")
+    if A.dim() != 2:
+        raise RuntimeError("A must be 2-D (no batch dimensions)")
+    M, K = A.shape
+    vals = A.values()
+    if M >= 2**31 - 1 or K > 2**31 - 1 or vals.numel() > 2**31 - 1:
+        raise RuntimeError("A's sizes must fit int32")
+    if vals.dtype != torch.float32:
+        raise RuntimeError("A_values must be float32")
+    rowptr = _C.indices_to_int32(A.crow_indices())
+    colidx = _C.indices_to_int32(A.col_indices())
+    return rowptr, colidx, vals.contiguous(), K
+
+
+def csrspmm_sparse(A, B, alpha=1.0, beta=0.0, algo="Auto"):
+    """C = alpha * A @ B for a torch.sparse_csr A (a new C; beta scales a zero
+    C, as in the five entry points)."""
+    rowptr, colidx, vals, K = from_sparse_csr(A)
+    if B.dim() != 2 or B.size(0) != K:
+        raise RuntimeError("B must be [K, N] with K = A.shape[1]")
+    return _C.csrspmm_forward(rowptr, colidx, vals, B, alpha, beta, algo)
+
+
+def dense_to_csr(D, tol=0.0):
+    """Device dense -> CSR (rowptr, colidx, values), keeping |v| > tol in
+    row-major order like the reference's host dense2csr; one host sync."""
+    return tuple(_C.dense_to_csr(D, float(tol)))
+
+
+def csr_max_row_nnz(rowptr):
+    """Longest row as a one-element int32 CUDA tensor (no host sync)."""
+    return _C.csr_max_row_nnz(rowptr)

@@ -187,6 +187,39 @@ int csrspmm_validate_csr(int M, int K, int nnz,
                          int* flags_out, int* max_row_nnz_out,
                          void* stream);
 
+/*
+ * Device-side CSR tooling, asynchronous on `stream` (no host sync).
+ *
+ * Dense -> CSR replaces the reference's host dense2csr
+ * (src/host/csr_utils.cpp:70-111) with the same rule: element (r, c) of the
+ * row-major M x K matrix `dense` (leading dimension ld >= K) is kept when
+ * fabsf(v) > tol, so +-0 and NaN are dropped, in row-major order.  Two steps,
+ * because the output size depends on the data:
+ *  1. csrspmm_dense2csr_count_f32 writes rowptr[0..M] and the nonzero count
+ *     as a 64-bit integer to *nnz_out (both device memory);
+ *  2. after allocating colidx and vals for that count (it must fit int32),
+ *     csrspmm_dense2csr_fill_f32 fills them.  Step 2 must see the same dense
+ *     values, tol and rowptr as step 1.
+ */
+int csrspmm_dense2csr_count_f32(int M, int K, const float* dense, long long ld, float tol,
+                                int* rowptr, long long* nnz_out, void* stream);
+int csrspmm_dense2csr_fill_f32(int M, int K, const float* dense, long long ld, float tol,
+                               const int* rowptr, int* colidx, float* vals, void* stream);
+
+/* *max_out (device memory) = the longest row of rowptr[0..M]: the
+ * max_row_nnz that the reference's dense2csr scans on the host
+ * (src/host/csr_utils.cpp:106-110) and its torch benchmark fetches with a
+ * host sync (torch_csrspmm/torch_benchmarks.py:39-44), here left on the device. */
+int csrspmm_csr_max_row_nnz(int M, const int* rowptr, int* max_out, void* stream);
+
+/* dst[i] = (int32)src[i] for i < n: int64 CSR indices (torch.sparse_csr's
+ * default) narrowed for this library's int32 kernels.  If overflow_out
+ * (device memory) is not NULL it is set to 1 when some value does not fit
+ * int32, else 0.  The reference accepts int32 only
+ * (torch_csrspmm/torch_csrspmm_naive.cpp:24-26). */
+int csrspmm_indices_i64_to_i32(const long long* src, int* dst, long long n, int* overflow_out,
+                               void* stream);
+
 /* Memory and device helpers that let the g++-built C++ layer stay free of
  * HIP headers (they back csr_alloc_device / dense_alloc_device and the
  * host<->device copies at reference src/host/csr_utils.cpp:44-67,183-238 and

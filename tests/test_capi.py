@@ -133,3 +133,14 @@ def test_validate_rejects_bad_sizes_without_device():
     lib = capi.hip()
     assert lib.csrspmm_validate_csr(-1, 4, 0, None, None, None, None, None) == -1
     assert lib.csrspmm_validate_csr(4, 4, 0, None, None, None, None, None) == -1
+
+
+def test_csr_tools_argument_errors_without_device():
+    lib = capi.hip()
+    inv = -1  # CSRSPMM_STATUS_INVALID_VALUE
+    assert lib.csrspmm_dense2csr_count_f32(-1, 4, None, 4, 0.0, None, None, None) == inv
+    assert lib.csrspmm_dense2csr_count_f32(4, 4, None, 4, 0.0, None, None, None) == inv
+    assert lib.csrspmm_dense2csr_fill_f32(4, 8, None, 4, 0.0, None, None, None, None) == inv
+    assert lib.csrspmm_csr_max_row_nnz(3, None, None, None) == inv
+    assert lib.csrspmm_indices_i64_to_i32(None, None, 5, None, None) == inv
+    assert lib.csrspmm_indices_i64_to_i32(None, None, -1, None, None) == inv

@@ -23,7 +23,8 @@ def test_cpp_test_driver_all_variants(args, gpu):
                        capture_output=True, text=True, timeout=120)
     print(r.stdout, r.stderr)
     assert r.returncode == 0
-    assert r.stdout.count("Pass: ") == 14  # 7 algorithms, each per call and through a plan
+    # 7 algorithms, each per call and through a plan, and the device dense2csr
+    assert r.stdout.count("Pass: ") == 15
     assert "Error" not in r.stdout
 
 

@@ -55,3 +55,14 @@ def test_extras_raise_on_host_tensors():
         tc.csrspmm_spmm_out(rowptr, colidx, vals, B, torch.zeros(2, 4), 1.0, 0.0)
     with pytest.raises(RuntimeError, match="CSR tensors must be CUDA tensors"):
         tc.CsrSpmmPlan(rowptr, colidx, vals, 2)
+
+
+@pytest.mark.filterwarnings("ignore:Sparse CSR tensor support")
+def test_sparse_csr_entry_checks_on_host():
+    A = torch.eye(3).to_sparse_csr()
+    with pytest.raises(RuntimeError, match="CUDA"):
+        tc.from_sparse_csr(A)
+    with pytest.raises(RuntimeError, match="sparse_csr"):
+        tc.from_sparse_csr(torch.eye(3))
+    with pytest.raises(RuntimeError, match="CUDA"):
+        tc.dense_to_csr(torch.eye(3))
