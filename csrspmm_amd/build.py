@@ -8,6 +8,7 @@ Targets (outputs under csrspmm_amd/lib/ and csrspmm_amd/torch_csrspmm/):
   host   libcsrspmm.so       g++: C++ API (include/csrspmm/*), generators
   torch  torch_csrspmm/_C.so g++: PyTorch-ROCm extension over the C ABI
   apps   test_csrspmm, bench_csrspmm   g++: C++ drivers over libcsrspmm.so
+  vendor libcsrspmm_vendor.so g++: rocSPARSE SpMM timing shim (comparison bench only)
 """
 from __future__ import annotations
 
@@ -120,11 +121,21 @@ def build_apps() -> list[str]:
     return outs
 
 
-TARGETS = {"hip": build_hip, "host": build_host, "torch": build_torch, "apps": build_apps}
+def build_vendor() -> str:
+    out = os.path.join(LIB, "libcsrspmm_vendor.so")
+    _run(["g++", *GXX_FLAGS, "-shared", "-D__HIP_PLATFORM_AMD__=1", "-isystem", "/opt/rocm/include",
+          os.path.join(CSRC, "vendor", "rocsparse_spmm_bench.cpp"), "-L", "/opt/rocm/lib",
+          "-lrocsparse", "-lamdhip64", "-Wl,-rpath,/opt/rocm/lib", "-o", out + ".tmp"])
+    os.replace(out + ".tmp", out)
+    return out
+
+
+TARGETS = {"hip": build_hip, "host": build_host, "torch": build_torch, "apps": build_apps,
+           "vendor": build_vendor}
 
 
 def build(targets: list[str] | None = None) -> None:
-    for t in targets or ["hip", "host", "torch", "apps"]:
+    for t in targets or list(TARGETS):
         TARGETS[t]()
 
 
