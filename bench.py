@@ -160,7 +160,8 @@ def main():
         "B": torch.from_numpy(B).to(dev),
         "C": torch.empty((a.M, N), dtype=torch.float32, device=dev),
     }
-    need = max(capi.hip().csrspmm_workspace_bytes(capi.ALGO[x], a.M, N, a.nnz) for x in ALGORITHMS)
+    need = max(capi.hip().csrspmm_workspace_bytes_ex(capi.ALGO[x], a.M, a.K, N, a.nnz, -1)
+               for x in ALGORITHMS)
     d["ws"] = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
     torch.cuda.synchronize()
 
@@ -238,7 +239,7 @@ def main():
                    "alpha": 1.0, "beta": 0.0, "bytes_alg": balg},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "kernel": f"{resolved} main kernel",
+                     "traffic": traffic, "kernel": f"{resolved}: all launches of one call",
                      "kernel_ms": round(main_ms, 5)},
         "cpu_baseline": cpu,
         "variants": variants,

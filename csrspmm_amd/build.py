@@ -26,7 +26,7 @@ LIB = os.path.join(PKG, "lib")
 INC = os.path.join(ROOT, "include")
 
 HIP_SOURCES = ["device/capi.hip", "device/rowgroup.hip", "device/naive.hip", "device/plan.hip",
-               "device/csr_tools.hip"]
+               "device/panels.hip", "device/csr_tools.hip"]
 HOST_SOURCES = ["host/csrspmm.cpp", "host/spmm_launcher.cpp", "host/csr_utils.cpp",
                 "host/dense_utils.cpp", "host/gen.cpp"]
 

@@ -29,6 +29,7 @@ HIP_API = {
     "csrspmm_algorithm_name": (ctypes.c_char_p, [_c_int]),
     "csrspmm_resolve_algorithm": (_c_int, [_c_int, _c_int]),
     "csrspmm_workspace_bytes": (_c_size_t, [_c_int, _c_int, _c_int, _c_int]),
+    "csrspmm_workspace_bytes_ex": (_c_size_t, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
     "csrspmm_spmm_f32": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p, _c_void_p,
                                   _c_void_p, _c_int, _c_void_p, _c_ll, _c_void_p, _c_ll, _c_float,
                                   _c_float, _c_void_p]),
@@ -154,7 +155,7 @@ def spmm(algo, rowptr, colidx, vals, B, C, alpha, beta, *, M=None, K=None, hint=
         st = lib.csrspmm_spmm_f32(a, M, K, N, nnz, _ptr(rowptr), _ptr(colidx), _ptr(vals), hint,
                                   _ptr(B), ldb, _ptr(C), ldc, alpha, beta, ctypes.c_void_p(stream))
     else:
-        need = lib.csrspmm_workspace_bytes(a, M, N, nnz)
+        need = lib.csrspmm_workspace_bytes_ex(a, M, K, N, nnz, hint)
         if workspace is None and need > 0:
             workspace = torch.empty(need, dtype=torch.uint8, device=C.device)
         wsz = 0 if workspace is None else workspace.numel()

@@ -18,7 +18,7 @@ namespace csrspmm_hip {
 
 static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-WorkspaceLayout workspace_layout(int M, int N, int nnz) {
+WorkspaceLayout workspace_layout(int M, int K, int N, int nnz, int P) {
   WorkspaceLayout L{};
   L.nslots = nnz / kSegLen;
   L.nblocks = (int)(((long long)M + nnz + 1 + kMergeBlock - 1) / kMergeBlock);
@@ -30,6 +30,29 @@ WorkspaceLayout workspace_layout(int M, int N, int nnz) {
   off = align256(off + (size_t)L.nslots * sizeof(int2));
   L.partials_off = off;
   off = align256(off + (size_t)L.nslots * (size_t)L.ldp * sizeof(float));
+  L.base_total = off;
+  if (P > 0 && K > 0) {
+    L.P = P;
+    L.width = (int)(((long long)K + P - 1) / P);
+    L.nwin = (int)(((long long)nnz + kPanelMinLen - 1) / kPanelMinLen);
+    const long long per_row = (long long)P * L.ldp * (long long)sizeof(float);
+    L.nl_max = (int)std::min<long long>(L.nwin, std::max<long long>(1, kDevPanelPartialBudget / per_row));
+    const size_t nw = (size_t)L.nwin;
+    L.win_row_off = off;
+    off = align256(off + nw * sizeof(int));
+    L.flag_off = off;
+    off = align256(off + nw * sizeof(int));
+    L.pidx_off = off;
+    off = align256(off + nw * sizeof(int));
+    L.list_off = off;
+    off = align256(off + (size_t)L.nl_max * sizeof(int));
+    L.bnd_off = off;
+    off = align256(off + nw * ((size_t)P + 1) * sizeof(int));
+    L.sched_off = off;
+    off = align256(off + (size_t)(kXcds + 2) * sizeof(int));
+    L.part_off = off;
+    off = align256(off + (size_t)L.nl_max * (size_t)P * (size_t)L.ldp * sizeof(float));
+  }
   L.total = off;
   return L;
 }
@@ -42,6 +65,26 @@ void bind_workspace(Problem& p, void* ws, const WorkspaceLayout& L) {
   p.ldp = L.ldp;
   p.nslots = L.nslots;
   p.nblocks = L.nblocks;
+  p.dp = DevPanels{};
+  if (L.P > 0) {
+    p.dp.P = L.P;
+    p.dp.width = L.width;
+    p.dp.nwin = L.nwin;
+    p.dp.nl_max = L.nl_max;
+    p.dp.win_row = reinterpret_cast<int*>(b + L.win_row_off);
+    p.dp.flag = reinterpret_cast<int*>(b + L.flag_off);
+    p.dp.pidx = reinterpret_cast<int*>(b + L.pidx_off);
+    p.dp.list = reinterpret_cast<int*>(b + L.list_off);
+    p.dp.bnd = reinterpret_cast<int*>(b + L.bnd_off);
+    p.dp.sched = reinterpret_cast<int*>(b + L.sched_off);
+    p.dp.part = reinterpret_cast<float*>(b + L.part_off);
+  }
+}
+
+int per_call_panels(int vec, bool plan, int K, int N, int nnz, int hint) {
+  if (vec != 4 || !plan || nnz < kPanelMinLen) return 0;
+  if (hint >= 0 && hint < kPanelMinLen) return 0;
+  return panel_count(K, N);
 }
 
 namespace {
@@ -188,13 +231,16 @@ int spmm_impl(int algo_in, int M, int K, int N, int nnz, const int* rowptr, cons
   hipStream_t s = static_cast<hipStream_t>(stream);
   p.plan = wants_plan(algo, M, nnz, hint);
   if (p.plan) {
-    const WorkspaceLayout L = workspace_layout(M, N, nnz);
+    const int P = per_call_panels(vector_width(algo, p), true, K, N, nnz, hint);
+    WorkspaceLayout L = workspace_layout(M, K, N, nnz, P);
     if (owned) {
       st = owned_workspace(stream, L.total, &ws);
       if (st != 0) return st;
     } else {
-      if (!ws || ws_bytes < L.total) return CSRSPMM_STATUS_WORKSPACE_TOO_SMALL;
+      if (!ws || ws_bytes < L.base_total) return CSRSPMM_STATUS_WORKSPACE_TOO_SMALL;
       if (reinterpret_cast<uintptr_t>(ws) & 255) return CSRSPMM_STATUS_INVALID_VALUE;
+      // a workspace sized without the panel tables runs without panels
+      if (ws_bytes < L.total) L = workspace_layout(M, K, N, nnz, 0);
     }
     bind_workspace(p, ws, L);
   }
@@ -335,7 +381,17 @@ int csrspmm_resolve_algorithm(int algo, int N) { return resolve_algorithm(algo, 
 size_t csrspmm_workspace_bytes(int algo, int M, int N, int nnz) {
   algo = resolve_algorithm(algo, N);
   if (M <= 0 || N <= 0 || nnz < 0 || !wants_plan(algo, M, nnz, -1)) return 0;
-  return workspace_layout(M, N, nnz).total;
+  return workspace_layout(M, 0, N, nnz, 0).base_total;
+}
+
+size_t csrspmm_workspace_bytes_ex(int algo, int M, int K, int N, int nnz, int max_row_nnz_hint) {
+  algo = resolve_algorithm(algo, N);
+  if (M <= 0 || N <= 0 || nnz < 0 || K < 0 || !wants_plan(algo, M, nnz, max_row_nnz_hint)) return 0;
+  // float4 columns as far as the shape tells (pointer alignment is checked per call)
+  const bool fp4 = (algo == CSRSPMM_ALGO_WARP_PER_ROW_FP4 || algo == CSRSPMM_ALGO_WARP_PER_ROW_SMEM_FP4) &&
+                   N % 4 == 0;
+  const int P = per_call_panels(fp4 ? 4 : 1, true, K, N, nnz, max_row_nnz_hint);
+  return workspace_layout(M, K, N, nnz, P).total;
 }
 
 int csrspmm_spmm_f32(int algo, int M, int K, int N, int nnz, const int* rowptr, const int* colidx,

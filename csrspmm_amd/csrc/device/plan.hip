@@ -30,12 +30,6 @@
 #include "common.hpp"
 #include "spmm_internal.h"
 
-#ifndef CSRSPMM_PANEL_MIN_LEN
-#define CSRSPMM_PANEL_MIN_LEN 2048
-#endif
-#ifndef CSRSPMM_PANEL_BAND_KB
-#define CSRSPMM_PANEL_BAND_KB 512
-#endif
 #ifndef CSRSPMM_PANEL_UNIT_ITEMS
 #define CSRSPMM_PANEL_UNIT_ITEMS 64
 #endif
@@ -43,22 +37,7 @@
 namespace csrspmm_hip {
 namespace {
 
-constexpr int kPanelMinLen = CSRSPMM_PANEL_MIN_LEN;
-constexpr long long kPanelBandBytes = (long long)CSRSPMM_PANEL_BAND_KB * 1024;
 constexpr int kPanelUnitItems = CSRSPMM_PANEL_UNIT_ITEMS;
-constexpr int kPanelMaxPanels = 256;
-constexpr int kPanelSkewMax = 4;  // max panel load over mean panel load
-
-// Panels for a K x N fp32 B: a power of two (>= kXcds) giving a band of about
-// kPanelBandBytes; 0 (off) when B is small enough for the L2s, N is wide, or
-// the band knob is 0.
-int panel_count(int K, int N) {
-  const long long bbytes = (long long)K * N * 4;
-  if (kPanelBandBytes <= 0 || N > 256 || bbytes < 16LL * 1024 * 1024) return 0;
-  long long p = kXcds;
-  while (p * 2 <= kPanelMaxPanels && p * 2 * kPanelBandBytes <= bbytes) p *= 2;
-  return (int)p;
-}
 
 // Groups (rows) per workgroup of the kernel launch_rowgroup picks for N.
 int groups_per_block(int vec, int N) {

@@ -55,12 +55,31 @@ constexpr int kVec4U = CSRSPMM_VEC4_UNROLL;
 #define CSRSPMM_SEG_UNROLL 4
 #endif
 
+// Workgroups per XCD of the pieces kernel (a persistent grid: about as many
+// as the XCD's 32 CUs hold at once).
+#ifndef CSRSPMM_PIECE_BLOCKS_PER_XCD
+#define CSRSPMM_PIECE_BLOCKS_PER_XCD 256
+#endif
+constexpr int kPieceBlocksPerXcd = CSRSPMM_PIECE_BLOCKS_PER_XCD;
+
 __device__ __forceinline__ void wave_lds_sync() {
   // The LDS stage is private to the wave: order its writes against the
   // group's reads (and the next chunk's overwrite) without a block barrier.
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ int clamp_nnz(int x, int nnz) { return min(max(x, 0), nnz); }
+
+// True when this call's column panels took the long row starting at
+// nonzero x0 (its segments are then skipped).
+__device__ __forceinline__ bool is_panelized(const Problem& p, int x0) {
+  if (p.dp.P <= 0) return false;
+  const int id = (clamp_nnz(x0, p.nnz) + kPanelMinLen - 1) / kPanelMinLen;
+  if (id >= p.dp.nwin) return false;
+  const int pi = p.dp.pidx[id];
+  return pi >= 0 && pi < p.dp.sched[0];
 }
 
 // Column bookkeeping of one panel of PW = G*VEC*T columns starting at c0.
@@ -231,6 +250,7 @@ __global__ __launch_bounds__(kWaves * 64) void rowgroup_kernel(Problem p, int se
       const int rs = p.rowptr[si.x];
       const int re = p.rowptr[si.x + 1];
       const int len = re - rs;
+      if (len >= kPanelMinLen && is_panelized(p, rs)) continue;  // summed by the pieces kernel
       const int nseg = len / kSegLen;
       const int start = rs + seg_begin(len, nseg, si.y);
       const int end = rs + seg_begin(len, nseg, si.y + 1);
@@ -290,7 +310,67 @@ __global__ __launch_bounds__(kWaves * 64) void rowgroup_kernel(Problem p, int se
   }
 }
 
-__device__ __forceinline__ int clamp_nnz(int x, int nnz) { return min(max(x, 0), nnz); }
+// Pieces of this call's column panels.  Workgroup b runs on XCD b mod kXcds
+// and shares with the other workgroups of that XCD the pieces of its panel
+// range [qa, qb): piece i is (panel qa + i / nl, panelized row i mod nl), the
+// nonzeros of that row whose columns fall in the panel, summed into the
+// partial (row, panel).  Pieces are dealt group-strided in panel order, so
+// the groups of an XCD work within a few panels at a time and gather from a
+// band of B that stays in that XCD's L2.  The grid is fixed; every group
+// leaves its loop when the pieces of its range run out.
+template <int VEC, int G, int T, int U, bool LDS>
+__global__ __launch_bounds__(kWaves * 64) void panel_pieces_kernel(Problem p) {
+  using VT = typename Vec<VEC>::T;
+  constexpr int GPW = 64 / G;
+  constexpr int GPB = kWaves * GPW;
+  constexpr int PW = G * VEC * T;
+  constexpr int US = CSRSPMM_SEG_UNROLL > U ? (CSRSPMM_SEG_UNROLL < G ? CSRSPMM_SEG_UNROLL : G) : U;
+  const DevPanels& d = p.dp;
+  const int nl = d.sched[0];
+  if (nl <= 0) return;
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int gl = lane & (G - 1);
+  const int gbase = lane & ~(G - 1);
+  const int gid = wave * GPW + lane / G;
+  __shared__ int2 stage_all[LDS ? kWaves * 64 : 1];
+  int2* stage = stage_all + (LDS ? wave * 64 : 0);
+
+  const int x = (int)blockIdx.x % kXcds;
+  const int jb = (int)blockIdx.x / kXcds;
+  const int nb = (int)gridDim.x / kXcds;
+  const int qa = d.sched[1 + x];
+  const int qb = d.sched[2 + x];
+  const unsigned npieces = (unsigned)max(qb - qa, 0) * (unsigned)nl;
+  for (unsigned i = (unsigned)(jb * GPB + gid); i < npieces; i += (unsigned)(nb * GPB)) {
+    const int q = qa + (int)(i / (unsigned)nl);
+    const int ri = (int)(i % (unsigned)nl);
+    const int id = d.list[ri];
+    const int r = d.win_row[id];
+    if (r < 0 || r >= p.M) continue;  // only for a malformed rowptr
+    const int x0 = clamp_nnz(p.rowptr[r], p.nnz);
+    const int x1 = max(x0, clamp_nnz(p.rowptr[r + 1], p.nnz));
+    const int* b = d.bnd + (long long)id * (d.P + 1);
+    const int a = min(max(b[q], x0), x1);
+    const int e = min(max(b[q + 1], a), x1);
+    float* prow = d.part + ((long long)ri * d.P + q) * p.ldp;
+    for (int c0 = 0; c0 < p.N; c0 += PW) {
+      const Panel<VEC, G, T> pn(p, c0, gl);
+      VT acc[T];
+#pragma unroll
+      for (int t = 0; t < T; ++t) acc[t] = Vec<VEC>::zero();
+      stream_nonzeros<VEC, G, T, US, LDS>(p, pn, a, e, gl, gbase, stage,
+                                          [&](int, float v, const VT(&bv)[T]) {
+#pragma unroll
+                                            for (int t = 0; t < T; ++t) acc[t] = fma_v(v, bv[t], acc[t]);
+                                          });
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        if (pn.cval[t]) *reinterpret_cast<VT*>(prow + pn.col[t]) = acc[t];
+      }
+    }
+  }
+}
 
 // One thread per row r in [0, M]: the merge-block starts that fall on r, and
 // the segment slots r owns.  Every entry the main kernel reads is written
@@ -317,6 +397,16 @@ __global__ __launch_bounds__(256) void plan_kernel(Problem p) {
     const int nseg = len > kLongRow ? len / kSegLen : 0;
     for (int s = s0; s < s1; ++s)
       p.seg_info[s] = (s - s0) < nseg ? make_int2(r, s - s0) : make_int2(-1, 0);
+    if (p.dp.P > 0) {
+      // windows w whose first position w * kPanelMinLen lies in this row; the
+      // first of them is the row's id when the row is long
+      const int w0 = (x0 + kPanelMinLen - 1) / kPanelMinLen;
+      const int w1 = min((x1 + kPanelMinLen - 1) / kPanelMinLen, p.dp.nwin);
+      for (int w = w0; w < w1; ++w) {
+        p.dp.win_row[w] = r;
+        p.dp.flag[w] = (w == w0 && len >= kPanelMinLen) ? 1 : 0;
+      }
+    }
   }
 }
 
@@ -395,8 +485,10 @@ __global__ __launch_bounds__(kWaves * 64) void combine_kernel(Problem p, int sca
         const int l = __ffsll((long long)firsts) - 1;
         firsts &= firsts - 1;
         const int row = __builtin_amdgcn_readlane(si.x, l);
-        const int nseg = (p.rowptr[row + 1] - p.rowptr[row]) / kSegLen;
+        const int len = p.rowptr[row + 1] - p.rowptr[row];
+        const int nseg = len / kSegLen;
         if (nseg < 2) continue;  // stored by the segment phase
+        if (len >= kPanelMinLen && is_panelized(p, p.rowptr[row])) continue;  // summed from pieces
         const float* base = p.partials + (long long)(ch * 64 + l) * p.ldp;
         float* crow = p.C + (long long)row * p.ldc;
         for (int c0 = 0; c0 < p.N; c0 += GC * VEC) {
@@ -410,17 +502,31 @@ __global__ __launch_bounds__(kWaves * 64) void combine_kernel(Problem p, int sca
     return;
   }
   const int i = (int)blockIdx.x - scan_blocks;
-  if (i >= p.npan) return;
   __shared__ VT wave_sum[kWaves][GC];
-  const int row = p.pan_rows[i];
-  const int npc = p.pan_ptr[i + 1] - p.pan_ptr[i];
-  const int* pieces = p.pan_piece + p.pan_ptr[i];
+  int row, npc;
+  const int* pieces;
+  const float* part;
+  if (p.dp.P > 0) {
+    // this call's panelized row i: partials (i, 0 .. P-1), in column order
+    if (i >= p.dp.sched[0]) return;
+    row = p.dp.win_row[p.dp.list[i]];
+    if (row < 0 || row >= p.M) return;  // only for a malformed rowptr
+    npc = p.dp.P;
+    pieces = nullptr;
+    part = p.dp.part + (long long)i * p.dp.P * p.ldp;
+  } else {
+    if (i >= p.npan) return;
+    row = p.pan_rows[i];
+    npc = p.pan_ptr[i + 1] - p.pan_ptr[i];
+    pieces = p.pan_piece + p.pan_ptr[i];
+    part = p.pan_part;
+  }
   float* crow = p.C + (long long)row * p.ldc;
   for (int c0 = 0; c0 < p.N; c0 += GC * VEC) {
     const int c = c0 + gl * VEC;
     const bool cv = c < p.N;
     const VT acc = wave_group_sum<GC>(
-        sum_strided<VEC, kWaves * P>(p.pan_part + c, pieces, npc, wave * P + q, p.ldp, cv));
+        sum_strided<VEC, kWaves * P>(part + c, pieces, npc, wave * P + q, p.ldp, cv));
     if (q == 0) wave_sum[wave][gl] = acc;
     __syncthreads();
     if (wave == 0 && q == 0 && cv) {
@@ -437,7 +543,7 @@ template <int VEC>
 void launch_combine(const Problem& p, hipStream_t s) {
   const int chunks = (p.N + VEC - 1) / VEC;
   const int scan_blocks = std::min(kCombineScanBlocks, div_up_host(div_up_host(p.nslots, 64), kWaves));
-  const int blocks = scan_blocks + p.npan;
+  const int blocks = scan_blocks + (p.dp.P > 0 ? p.dp.nl_max : p.npan);
   if (blocks == 0) return;
   if (chunks <= 8) {
     hipLaunchKernelGGL((combine_kernel<VEC, 8>), dim3(blocks), dim3(kWaves * 64), 0, s, p, scan_blocks);
@@ -458,13 +564,17 @@ hipError_t launch_rg(const Problem& p, hipStream_t s) {
   const int seg_blocks =
       (p.plan && p.nslots > 0) ? std::min(kSegBlocksMax, div_up_host(p.nslots, GPB)) : 0;
   const long long blocks = (long long)unit_blocks + seg_blocks;
-  if (blocks == 0) return hipSuccess;
-  timing_before_main(s);
+  if constexpr (VEC == 4) {  // panels are built for float4 columns only
+    if (p.dp.P > 0) {
+      // the pieces of panelized rows first, alone, so nothing else evicts their bands
+      hipLaunchKernelGGL((panel_pieces_kernel<VEC, G, T, U, LDS>), dim3(kXcds * kPieceBlocksPerXcd),
+                         dim3(kWaves * 64), 0, s, p);
+    }
+  }
+  if (blocks == 0) return hipGetLastError();
   hipLaunchKernelGGL((rowgroup_kernel<VEC, G, T, U, LDS>), dim3((unsigned)blocks), dim3(kWaves * 64),
                      0, s, p, seg_blocks);
-  const hipError_t e = hipGetLastError();
-  timing_after_main(s);
-  return e;
+  return hipGetLastError();
 }
 
 }  // namespace
@@ -512,20 +622,23 @@ static hipError_t dispatch_vec1(const Problem& p, hipStream_t s) {
   return launch_rg<1, 64, 8, 4, LDS>(p, s);  // N > 512 loops over 512-column panels
 }
 
-hipError_t launch_rowgroup(const Problem& p, int vec, bool lds, hipStream_t s) {
-  if (p.M == 0 || p.N == 0) return hipSuccess;
+static hipError_t launch_rowgroup_all(const Problem& p, int vec, bool lds, hipStream_t s) {
   if (p.plan && !p.plan_ready) {
     const int pblocks = std::min(div_up_host(p.M + 1, 256), 4096);
     hipLaunchKernelGGL(plan_kernel, dim3(pblocks), dim3(256), 0, s, p);
   }
   hipError_t e;
+  if (p.dp.P > 0) {
+    e = launch_panel_schedule(p, s);
+    if (e != hipSuccess) return e;
+  }
   if (vec == 4) {
     e = lds ? dispatch_vec4<true>(p, s) : dispatch_vec4<false>(p, s);
   } else {
     e = lds ? dispatch_vec1<true>(p, s) : dispatch_vec1<false>(p, s);
   }
   if (e != hipSuccess) return e;
-  if (p.plan && p.nslots + p.npan > 0) {
+  if (p.plan && (p.nslots + p.npan > 0 || p.dp.P > 0)) {
     if (vec == 4) {
       launch_combine<4>(p, s);
     } else {
@@ -533,6 +646,14 @@ hipError_t launch_rowgroup(const Problem& p, int vec, bool lds, hipStream_t s) {
     }
     e = hipGetLastError();
   }
+  return e;
+}
+
+hipError_t launch_rowgroup(const Problem& p, int vec, bool lds, hipStream_t s) {
+  if (p.M == 0 || p.N == 0) return hipSuccess;
+  timing_before_main(s);
+  const hipError_t e = launch_rowgroup_all(p, vec, lds, s);
+  timing_after_main(s);
   return e;
 }
 

@@ -63,6 +63,56 @@ constexpr long long kPlanMinItems = 1 << 16;
 // workgroup id, which stored plans use for L2 locality (plan.hip).
 constexpr int kXcds = 8;
 
+// Column panels.  A row of at least kPanelMinLen nonzeros with sorted
+// columns, on a B of at least 16 MiB with N <= 256 and float4 columns, is cut
+// at the boundaries of P column panels (P a power of two, kXcds..256, so that
+// a panel's band of B is about kPanelBandBytes).  Each XCD walks its own
+// panels in column order, so the band it gathers from stays in its L2.  Stored
+// plans build the schedule on the host (plan.hip); the per-call path builds
+// it on the device (panels.hip).
+#ifndef CSRSPMM_PANEL_MIN_LEN
+#define CSRSPMM_PANEL_MIN_LEN 2048
+#endif
+#ifndef CSRSPMM_PANEL_BAND_KB
+#define CSRSPMM_PANEL_BAND_KB 512
+#endif
+constexpr int kPanelMinLen = CSRSPMM_PANEL_MIN_LEN;
+constexpr long long kPanelBandBytes = (long long)CSRSPMM_PANEL_BAND_KB * 1024;
+constexpr int kPanelMaxPanels = 256;
+constexpr int kPanelSkewMax = 4;  // panels stay off when max panel load > 4 x mean
+static_assert(kPanelMinLen > kLongRow, "panelized rows are long rows");
+
+// Panels for a K x N fp32 B: a power of two (>= kXcds) giving a band of about
+// kPanelBandBytes; 0 (off) when B is small enough for the L2s or N is wide.
+inline int panel_count(int K, int N) {
+  const long long bbytes = (long long)K * N * 4;
+  if (kPanelBandBytes <= 0 || N > 256 || bbytes < 16LL * 1024 * 1024) return 0;
+  long long p = kXcds;
+  while (p * 2 <= kPanelMaxPanels && p * 2 * kPanelBandBytes <= bbytes) p *= 2;
+  return (int)p;
+}
+
+// Per-call column panels, built on the device each call (panels.hip) from the
+// CSR alone.  Positions of A's nonzeros are cut into windows of kPanelMinLen;
+// a row of len >= kPanelMinLen contains the start of window
+// id(r) = ceil(rowptr[r] / kPanelMinLen), which no other such row does, so
+// id(r) names the row in the per-window tables below.
+constexpr long long kDevPanelPartialBudget = 256LL << 20;  // bytes of piece partials, at most
+constexpr int kDevPanelSample = 64;  // rows sampled for the panel loads
+struct DevPanels {
+  int P;           // panels; 0 = off
+  int width;       // columns per panel, ceil(K / P)
+  int nwin;        // windows, ceil(nnz / kPanelMinLen)
+  int nl_max;      // panelized rows at most (rows of the partial buffer)
+  int* win_row;    // [nwin] the row holding position w * kPanelMinLen
+  int* flag;       // [nwin] 1: w = id(r) of a long row whose columns are sorted and in range
+  int* pidx;       // [nwin] compact index of the panelized row with id w, else -1
+  int* list;       // [nl_max] ids of the panelized rows, in row order
+  int* bnd;        // [nwin][P + 1] absolute position where panel q starts in the row with id w
+  int* sched;      // [0] = nl (0: no row panelized this call), [1 .. kXcds + 1] = XCD panel ranges
+  float* part;     // [nl_max][P][ldp] piece partial sums
+};
+
 // Cap on the blocks of the segment phase.  By default every segment slot
 // gets its own group, so the hardware dispatcher balances segments across
 // CUs; a smaller cap makes the segment blocks persistent (grid-strided).
@@ -102,15 +152,24 @@ struct Problem {
   const int* pan_ptr;
   const int* pan_piece;
   const float* pan_part;
+  // Per-call column panels (dp.P == 0: off).
+  DevPanels dp;
 };
 
-// Workspace layout for a problem (all offsets 256-byte aligned).
+// Workspace layout for a problem (all offsets 256-byte aligned).  P > 0 adds
+// the per-call panel tables and partial buffer after the base sections.
 struct WorkspaceLayout {
-  size_t block_start_off, seg_info_off, partials_off, total;
+  size_t block_start_off, seg_info_off, partials_off, base_total;
+  size_t win_row_off, flag_off, pidx_off, list_off, bnd_off, sched_off, part_off, total;
   int nslots, nblocks;
   long long ldp;
+  int P, width, nwin, nl_max;
 };
-WorkspaceLayout workspace_layout(int M, int N, int nnz);
+WorkspaceLayout workspace_layout(int M, int K, int N, int nnz, int P);
+
+// Panels the per-call path uses for this problem (0: none): float4 columns,
+// the plan on, and a row of kPanelMinLen nonzeros possible under the hint.
+int per_call_panels(int vec, bool plan, int K, int N, int nnz, int hint);
 
 // Bind the plan pointers of p into a workspace base pointer.
 void bind_workspace(Problem& p, void* ws, const WorkspaceLayout& L);
@@ -129,6 +188,11 @@ hipError_t launch_naive(const Problem& p, hipStream_t s);
 hipError_t launch_naive_smem(const Problem& p, hipStream_t s);
 // vec = 1 (scalar columns) or 4 (float4 columns); lds = stage (col,val) in LDS.
 hipError_t launch_rowgroup(const Problem& p, int vec, bool lds, hipStream_t s);
+
+// Per-call panel schedule (panels.hip): after plan_kernel has filled
+// dp.win_row / dp.flag, find the panel boundaries of the long rows, then
+// compact the panelized rows and deal the panels to the XCDs.
+hipError_t launch_panel_schedule(const Problem& p, hipStream_t s);
 
 // Benchmark timing hook: no-ops unless csrspmm_timing_enable(1) was called.
 // Calls nest (per thread): only the outermost before/after pair records, so

@@ -66,7 +66,7 @@ Tensor forward(int algo, const Tensor& rowptr, const Tensor& colidx, const Tenso
   if (M == 0 || N == 0) return C;
 
   const long long ldb = B.size(1) <= 1 ? std::max<long long>(N, 1) : B.stride(0);
-  const size_t ws_bytes = csrspmm_workspace_bytes(algo, M, N, nnz);
+  const size_t ws_bytes = csrspmm_workspace_bytes_ex(algo, M, K, N, nnz, hint);
   Tensor ws;
   void* ws_ptr = nullptr;
   if (ws_bytes > 0) {
@@ -148,7 +148,7 @@ Tensor csrspmm_spmm_out(Tensor A_row_ptr, Tensor A_col_idx, Tensor A_values, Ten
   const int nnz = static_cast<int>(A_values.size(0));
   if (M == 0 || N == 0) return C;
   const int a = algo_id(algo);
-  const size_t ws_bytes = csrspmm_workspace_bytes(a, M, N, nnz);
+  const size_t ws_bytes = csrspmm_workspace_bytes_ex(a, M, K, N, nnz, -1);
   Tensor ws;
   if (ws_bytes > 0) ws = torch::empty({static_cast<int64_t>(ws_bytes)}, B.options().dtype(torch::kUInt8));
   hipStream_t stream = c10::hip::getCurrentHIPStream(B.device().index()).stream();

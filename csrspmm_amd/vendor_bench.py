@@ -98,7 +98,7 @@ def main(argv=None):
             print(json.dumps(r), flush=True)
 
         ours_C = torch.empty((a.M, N), device=dev)
-        ws = torch.empty(max(capi.hip().csrspmm_workspace_bytes(capi.ALGO["Auto"], a.M, N, a.nnz),
+        ws = torch.empty(max(capi.hip().csrspmm_workspace_bytes_ex(capi.ALGO["Auto"], a.M, a.K, N, a.nnz, -1),
                              1), dtype=torch.uint8, device=dev)
         ms = timed(torch, lambda: capi.spmm("Auto", rp, ci, va, dB, ours_C, 1.0, 0.0, workspace=ws),
                    args.reps)

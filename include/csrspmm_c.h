@@ -84,6 +84,14 @@ int csrspmm_resolve_algorithm(int algo, int N);
  * the reference, which has no long-row splitting. */
 size_t csrspmm_workspace_bytes(int algo, int M, int N, int nnz);
 
+/* As csrspmm_workspace_bytes, plus the per-call column-panel tables and
+ * partial sums that float4 variants use for rows of >= 2048 nonzeros when B
+ * (K x N fp32) is >= 16 MiB and N <= 256 (at most 256 MiB of partials).  A
+ * max_row_nnz_hint in [0, 2048) (or -1: unknown) tells that no such row
+ * exists.  csrspmm_spmm_f32_ex given a workspace of at least
+ * csrspmm_workspace_bytes but less than this size runs without panels. */
+size_t csrspmm_workspace_bytes_ex(int algo, int M, int K, int N, int nnz, int max_row_nnz_hint);
+
 /*
  * The SpMM.  Replaces csrspmm::spmm's dispatch to launch_<variant>
  * (reference src/csrspmm.cpp:28-71, src/host/spmm_launcher.cu:11-171) and the

@@ -144,3 +144,22 @@ def test_csr_tools_argument_errors_without_device():
     assert lib.csrspmm_csr_max_row_nnz(3, None, None, None) == inv
     assert lib.csrspmm_indices_i64_to_i32(None, None, 5, None, None) == inv
     assert lib.csrspmm_indices_i64_to_i32(None, None, -1, None, None) == inv
+
+
+def test_workspace_bytes_ex_panels():
+    """The panel tables are reserved only for float4 variants on a B of
+    >= 16 MiB when a row of >= 2048 nonzeros is possible under the hint."""
+    lib = capi.hip()
+    a = capi.ALGO["WarpPerRowSmemFp4"]
+    M, K, N, nnz = 262144, 262144, 128, 8453223
+    base = lib.csrspmm_workspace_bytes(a, M, N, nnz)
+    assert lib.csrspmm_workspace_bytes_ex(a, M, K, N, nnz, 2047) == base
+    full = lib.csrspmm_workspace_bytes_ex(a, M, K, N, nnz, -1)
+    assert full == lib.csrspmm_workspace_bytes_ex(a, M, K, N, nnz, 16384) > base
+    # partials at most 256 MiB, plus tables of a few MiB
+    assert full - base <= (256 << 20) + (8 << 20)
+    s = capi.ALGO["WarpPerRowSmem"]
+    assert lib.csrspmm_workspace_bytes_ex(s, M, K, N, nnz, -1) == lib.csrspmm_workspace_bytes(s, M, N, nnz)
+    assert lib.csrspmm_workspace_bytes_ex(a, M, 1024, N, nnz, -1) == base  # B of 512 KiB
+    assert lib.csrspmm_workspace_bytes_ex(a, M, K, 512, nnz, -1) == lib.csrspmm_workspace_bytes(a, M, 512, nnz)
+    assert lib.csrspmm_workspace_bytes_ex(capi.ALGO["Naive"], M, K, N, nnz, -1) == 0

@@ -1,0 +1,166 @@
+"""GPU parity of the per-call column panels.
+
+With float4 columns (WarpPerRowFp4 / WarpPerRowSmemFp4 / Auto at N >= 128),
+a B of at least 16 MiB and N <= 256, every SpMM call cuts rows of >= 2048
+nonzeros with sorted columns at column-panel boundaries on the device, sums
+the pieces panel by panel (each XCD walking its own panels) and adds a
+row's pieces in column order.  These tests put such rows next to the cases
+that must fall back to the ordinary long-row segments (unsorted columns,
+skewed panel loads, a workspace sized without the panel tables) and check
+every row against the fp64 oracle at the 1e-5 bar, plus bitwise agreement
+with the fp32 CSR-order restatement on rows of <= 511 nonzeros.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from csrspmm_amd import ALGORITHMS, capi, gen
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+PANEL_ALGOS = ["WarpPerRowFp4", "WarpPerRowSmemFp4", "Auto"]
+
+
+def csr_from_lengths(lens, K, seed, narrow=None, unsorted_rows=()):
+    """Rows of the given lengths, columns uniform without replacement in
+    [0, K) (or in narrow[r] = (lo, hi) for chosen rows), sorted unless the
+    row is in unsorted_rows; values U(-1, 1) exact in fp32."""
+    rng = np.random.default_rng(seed)
+    lens = np.asarray(lens, dtype=np.int64)
+    rowptr = np.zeros(lens.size + 1, dtype=np.int32)
+    rowptr[1:] = np.cumsum(lens)
+    cols = []
+    for r, L in enumerate(lens):
+        lo, hi = (narrow or {}).get(r, (0, K))
+        c = rng.choice(hi - lo, size=int(L), replace=False).astype(np.int32) + lo
+        c.sort()
+        if r in unsorted_rows:
+            rng.shuffle(c)
+        cols.append(c)
+    colidx = np.concatenate(cols) if cols else np.zeros(0, np.int32)
+    vals = (rng.integers(0, 1 << 24, size=colidx.size) * 2.0 ** -23 - 1.0).astype(np.float32)
+    return rowptr, colidx.astype(np.int32), vals
+
+
+def mixed_lengths(seed, M=3000):
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(0, 40, size=M)
+    special = [2047, 2048, 2049, 3000, 4096, 5000, 20000, 256, 257, 511, 512, 767, 768, 0, 1, 16384]
+    pos = rng.choice(M, size=len(special), replace=False)
+    lens[pos] = special
+    lens[-1] = 6000  # a long row at the very end
+    return lens
+
+
+def run(algo, rowptr, colidx, vals, B, dev, C0=None, alpha=1.0, beta=0.0, workspace_bytes=None):
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)  # noqa: E731
+    drp, dci, dv, dB = t(rowptr), t(colidx), t(vals), t(B)
+    M, N = rowptr.size - 1, B.shape[1]
+    dC = t(C0) if C0 is not None else torch.full((M, N), float("nan"), device=dev)
+    ws = None
+    if workspace_bytes is not None:
+        ws = torch.empty(max(workspace_bytes, 1), dtype=torch.uint8, device=dev)
+    capi.spmm(algo, drp, dci, dv, dB, dC, alpha, beta, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(dci.cpu(), torch.from_numpy(colidx))
+    return dC.cpu().numpy()
+
+
+def check(algo, C, rowptr, colidx, vals, B, C0=None, alpha=1.0, beta=0.0, what=""):
+    assert not np.isnan(C).any(), f"{algo} {what}: unwritten output"
+    R, S = oracle.spmm_f64(rowptr, colidx, vals, B, C0, alpha, beta)
+    bad, ratio, _, _ = oracle.check(C, R, S, TOL)
+    assert bad == 0, f"{algo} {what}: {bad} elements off (max ratio {ratio:.3g})"
+    F = oracle.spmm_f32_seq(rowptr, colidx, vals, B, C0, alpha, beta)
+    whole = np.diff(rowptr) <= 511
+    assert np.array_equal(C[whole].view(np.uint32), F[whole].view(np.uint32)), \
+        f"{algo} {what}: short rows differ from the fp32 restatement"
+
+
+def panel_bytes(algo, M, K, N, nnz):
+    lib = capi.hip()
+    a = capi.ALGO[algo]
+    return lib.csrspmm_workspace_bytes(a, M, N, nnz), lib.csrspmm_workspace_bytes_ex(a, M, K, N, nnz, -1)
+
+
+@pytest.mark.parametrize("N", [64, 128, 256])
+@pytest.mark.parametrize("algo", list(ALGORITHMS) + ["Auto"])
+def test_panels_mixed_rows(algo, N, gpu):
+    K = 65536 if N == 64 else 32768  # B = 16 MiB (32 panels) or 16/32 MiB
+    lens = mixed_lengths(7 + N)
+    narrow = {int(np.nonzero(lens == 4096)[0][0]): (K // 3, K // 3 + 5000)}  # one panel-ish band
+    rowptr, colidx, vals = csr_from_lengths(lens, K, seed=N, narrow=narrow)
+    B = gen.dense(11, gen.TAG_B, K, N)
+    print(f"[panels] mixed {algo} N={N} M={lens.size} nnz={colidx.size}", flush=True)
+    base, full = panel_bytes(algo, lens.size, K, N, colidx.size)
+    if algo in ("WarpPerRowFp4", "WarpPerRowSmemFp4") or (algo == "Auto" and N >= 128):
+        assert full > base, "float4 variants on a 16 MiB B reserve the panel tables"
+    C = run(algo, rowptr, colidx, vals, B, gpu)
+    check(algo, C, rowptr, colidx, vals, B, what=f"mixed N={N}")
+    # repeated calls are bit-identical (no atomics in the float path)
+    C2 = run(algo, rowptr, colidx, vals, B, gpu)
+    assert np.array_equal(C.view(np.uint32), C2.view(np.uint32))
+
+
+@pytest.mark.parametrize("algo", PANEL_ALGOS)
+def test_panels_epilogue_and_strided_b(algo, gpu):
+    K, N = 65536, 128
+    lens = mixed_lengths(21, M=1500)
+    rowptr, colidx, vals = csr_from_lengths(lens, K, seed=21)
+    Bw = gen.dense(12, gen.TAG_B, K, N + 4)
+    B = Bw[:, :N]  # leading dimension N + 4 (padded rows)
+    C0 = gen.dense(12, gen.TAG_C0, lens.size, N)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(gpu)  # noqa: E731
+    dBw = t(Bw)
+    dB = dBw[:, :N]
+    dC = t(C0)
+    capi.spmm(algo, t(rowptr), t(colidx), t(vals), dB, dC, 0.75, -1.25)
+    torch.cuda.synchronize()
+    check(algo, dC.cpu().numpy(), rowptr, colidx, vals, np.ascontiguousarray(B), C0, 0.75, -1.25,
+          what="beta != 0, ldb = N + 4")
+
+
+@pytest.mark.parametrize("algo", PANEL_ALGOS)
+def test_panels_unsorted_row_falls_back(algo, gpu):
+    K, N = 65536, 128
+    lens = mixed_lengths(33)
+    r_uns = int(np.nonzero(lens == 5000)[0][0])
+    rowptr, colidx, vals = csr_from_lengths(lens, K, seed=33, unsorted_rows={r_uns})
+    B = gen.dense(13, gen.TAG_B, K, N)
+    C = run(algo, rowptr, colidx, vals, B, gpu)
+    check(algo, C, rowptr, colidx, vals, B, what="one unsorted long row")
+
+
+@pytest.mark.parametrize("algo", PANEL_ALGOS)
+def test_panels_skewed_loads_fall_back(algo, gpu):
+    # every long row gathers from the first 1/16 of the columns: two of the
+    # 32 panels carry all the load, so the call keeps the rows on segments
+    K, N = 65536, 128  # 32 panels of 2048 columns
+    rng = np.random.default_rng(44)
+    lens = rng.integers(0, 40, size=3000)
+    lens[rng.choice(3000, size=12, replace=False)] = [2048, 2049, 2500, 3000, 3500, 4000] * 2
+    narrow = {r: (0, 4096) for r in np.nonzero(lens >= 2048)[0].tolist()}
+    rowptr, colidx, vals = csr_from_lengths(lens, K, seed=44, narrow=narrow)
+    B = gen.dense(14, gen.TAG_B, K, N)
+    C = run(algo, rowptr, colidx, vals, B, gpu)
+    check(algo, C, rowptr, colidx, vals, B, what="skewed panel loads")
+
+
+@pytest.mark.parametrize("algo", PANEL_ALGOS)
+def test_panels_base_workspace_runs_without_panels(algo, gpu):
+    K, N = 65536, 128
+    lens = mixed_lengths(55)
+    rowptr, colidx, vals = csr_from_lengths(lens, K, seed=55)
+    B = gen.dense(15, gen.TAG_B, K, N)
+    base, full = panel_bytes(algo, lens.size, K, N, colidx.size)
+    assert full > base
+    C_base = run(algo, rowptr, colidx, vals, B, gpu, workspace_bytes=base)
+    check(algo, C_base, rowptr, colidx, vals, B, what="base-size workspace")
+    C_full = run(algo, rowptr, colidx, vals, B, gpu, workspace_bytes=full)
+    check(algo, C_full, rowptr, colidx, vals, B, what="panel-size workspace")
+    # rows summed whole agree bit for bit whichever way the long rows went
+    whole = np.diff(rowptr) <= 511
+    assert np.array_equal(C_base[whole].view(np.uint32), C_full[whole].view(np.uint32))
+
