@@ -21,7 +21,7 @@ static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 WorkspaceLayout workspace_layout(int M, int K, int N, int nnz, int P) {
   WorkspaceLayout L{};
   L.nslots = nnz / kSegLen;
-  L.nblocks = (int)(((long long)M + nnz + 1 + kMergeBlock - 1) / kMergeBlock);
+  L.nblocks = merge_blocks(M, nnz, kMergeBlockMin);  // capacity for any merge block size
   L.ldp = ((long long)N + 3) & ~3LL;
   size_t off = 0;
   L.block_start_off = off;
@@ -38,10 +38,8 @@ WorkspaceLayout workspace_layout(int M, int K, int N, int nnz, int P) {
     const long long per_row = (long long)P * L.ldp * (long long)sizeof(float);
     L.nl_max = (int)std::min<long long>(L.nwin, std::max<long long>(1, kDevPanelPartialBudget / per_row));
     const size_t nw = (size_t)L.nwin;
-    L.win_row_off = off;
-    off = align256(off + nw * sizeof(int));
-    L.flag_off = off;
-    off = align256(off + nw * sizeof(int));
+    L.win_off = off;
+    off = align256(off + nw * sizeof(int4));
     L.pidx_off = off;
     off = align256(off + nw * sizeof(int));
     L.list_off = off;
@@ -57,22 +55,22 @@ WorkspaceLayout workspace_layout(int M, int K, int N, int nnz, int P) {
   return L;
 }
 
-void bind_workspace(Problem& p, void* ws, const WorkspaceLayout& L) {
+void bind_workspace(Problem& p, void* ws, const WorkspaceLayout& L, int mblk) {
   char* b = static_cast<char*>(ws);
   p.block_start = reinterpret_cast<int*>(b + L.block_start_off);
   p.seg_info = reinterpret_cast<int2*>(b + L.seg_info_off);
   p.partials = reinterpret_cast<float*>(b + L.partials_off);
   p.ldp = L.ldp;
   p.nslots = L.nslots;
-  p.nblocks = L.nblocks;
+  p.mblk = mblk;
+  p.nblocks = merge_blocks(p.M, p.nnz, mblk);
   p.dp = DevPanels{};
   if (L.P > 0) {
     p.dp.P = L.P;
     p.dp.width = L.width;
     p.dp.nwin = L.nwin;
     p.dp.nl_max = L.nl_max;
-    p.dp.win_row = reinterpret_cast<int*>(b + L.win_row_off);
-    p.dp.flag = reinterpret_cast<int*>(b + L.flag_off);
+    p.dp.win = reinterpret_cast<int4*>(b + L.win_off);
     p.dp.pidx = reinterpret_cast<int*>(b + L.pidx_off);
     p.dp.list = reinterpret_cast<int*>(b + L.list_off);
     p.dp.bnd = reinterpret_cast<int*>(b + L.bnd_off);
@@ -187,7 +185,7 @@ int fill_problem(Problem& p, int algo, int M, int K, int N, int nnz, const int* 
   if (nnz > 0 && (!colidx || !vals || !B || K == 0)) return CSRSPMM_STATUS_INVALID_VALUE;
   if (ldc < N || (nnz > 0 && ldb < N)) return CSRSPMM_STATUS_INVALID_VALUE;
   // Merge coordinates (row + nonzero index) and grid sizes must fit int32.
-  if ((long long)M + nnz + 1 > 0x7fffffffLL - kMergeBlock) return CSRSPMM_STATUS_NOT_SUPPORTED;
+  if ((long long)M + nnz + 1 > 0x7fffffffLL - kMergeBlockMax) return CSRSPMM_STATUS_NOT_SUPPORTED;
   p.rowptr = rowptr;
   p.colidx = colidx;
   p.vals = vals;
@@ -231,7 +229,8 @@ int spmm_impl(int algo_in, int M, int K, int N, int nnz, const int* rowptr, cons
   hipStream_t s = static_cast<hipStream_t>(stream);
   p.plan = wants_plan(algo, M, nnz, hint);
   if (p.plan) {
-    const int P = per_call_panels(vector_width(algo, p), true, K, N, nnz, hint);
+    const int vec = vector_width(algo, p);
+    const int P = per_call_panels(vec, true, K, N, nnz, hint);
     WorkspaceLayout L = workspace_layout(M, K, N, nnz, P);
     if (owned) {
       st = owned_workspace(stream, L.total, &ws);
@@ -242,7 +241,7 @@ int spmm_impl(int algo_in, int M, int K, int N, int nnz, const int* rowptr, cons
       // a workspace sized without the panel tables runs without panels
       if (ws_bytes < L.total) L = workspace_layout(M, K, N, nnz, 0);
     }
-    bind_workspace(p, ws, L);
+    bind_workspace(p, ws, L, merge_block(vec));
   }
   return to_status(launch_algorithm(algo, p, s));
 }

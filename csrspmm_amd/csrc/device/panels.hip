@@ -6,11 +6,11 @@
 // schedule inside each SpMM call, in two launches after plan_kernel:
 //
 //  1. panel_window_kernel, one wave per window of kPanelMinLen nonzero
-//     positions.  A long row covering part of window w is win_row[w] or
-//     win_row[w + 1] (a row that starts inside the window also holds the
+//     positions.  A long row covering part of window w is the row of win[w]
+//     or of win[w + 1] (a row that starts inside the window also holds the
 //     start of the next one), so each wave checks at most two rows.  Over its
 //     share of a long row it checks that the columns are in range and
-//     non-decreasing (any violation clears flag[id]), and records where each
+//     non-decreasing (any violation clears the flag of win[id]), and records where each
 //     panel starts: bnd[id][q] = the first position whose column lies in
 //     panel q or later (the row end when there is none).  With sorted
 //     columns every q in [0, P] is written exactly once, by the wave that
@@ -47,44 +47,65 @@ __global__ __launch_bounds__(256) void panel_window_kernel(Problem p) {
   if (w >= d.nwin) return;
   const int pos0 = w * kPanelMinLen;
   const int pos1 = min(pos0 + kPanelMinLen, p.nnz);
-  const int cand[2] = {d.win_row[w], w + 1 < d.nwin ? d.win_row[w + 1] : -1};
+  const int4 wa = d.win[w];
+  const int4 wb = w + 1 < d.nwin ? d.win[w + 1] : make_int4(-1, 0, 0, 0);
   for (int c = 0; c < 2; ++c) {
-    const int r = cand[c];
-    if (r < 0 || r >= p.M || (c == 1 && r == cand[0])) continue;
-    const int x0 = clampi(p.rowptr[r], 0, p.nnz);
-    const int x1 = clampi(p.rowptr[r + 1], x0, p.nnz);
+    const int4 wi = c == 0 ? wa : wb;
+    const int r = wi.x;
+    if (r < 0 || r >= p.M || (c == 1 && r == wa.x)) continue;
+    const int x0 = clampi(wi.y, 0, p.nnz);
+    const int x1 = clampi(wi.z, x0, p.nnz);
     if (x1 - x0 < kPanelMinLen) continue;
     const int id = (x0 + kPanelMinLen - 1) / kPanelMinLen;
-    if (id >= d.nwin || d.win_row[id] != r) continue;  // only for a malformed rowptr
     const int lo = max(pos0, x0);
     const int hi = min(pos1, x1);
+    if (id >= d.nwin || lo >= hi) continue;
     int* bnd = d.bnd + (long long)id * (d.P + 1);
+    // this row's columns in the window, all loads in flight at once; the
+    // previous column of lane l is lane l-1's (lane 0: the carry)
+    constexpr int kC = kPanelMinLen / 64;
+    int cv[kC];
+#pragma unroll
+    for (int u = 0; u < kC; ++u) {
+      const int j = lo + u * 64 + lane;
+      cv[u] = j < hi ? p.colidx[j] : 0;
+    }
+    int carry = lo > x0 ? p.colidx[lo - 1] : -1;
     bool bad = false;
-    for (int j0 = lo; j0 < hi; j0 += 8 * 64) {
-      int cj[8], pv[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {  // 16 loads in flight per lane
-        const int j = j0 + u * 64 + lane;
-        cj[u] = j < hi ? p.colidx[j] : 0;
-        pv[u] = (j < hi && j > x0) ? p.colidx[j - 1] : -1;
-      }
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int j = j0 + u * 64 + lane;
-        if (j >= hi) continue;
-        if (cj[u] < 0 || cj[u] >= p.K || pv[u] > cj[u]) {
+    for (int u = 0; u < kC; ++u) {
+      const int j = lo + u * 64 + lane;
+      int prev = __shfl_up(cv[u], 1);
+      const int last = __shfl(cv[u], 63);
+      if (lane == 0) prev = carry;
+      carry = last;
+      if (j < hi) {
+        const int cj = cv[u];
+        const bool first = j == x0;
+        if (cj < 0 || cj >= p.K || (!first && prev > cj)) {
           bad = true;
-          continue;
+        } else {
+          const int q1 = cj / d.width;                                // panel of this column
+          const int q0 = first ? -1 : clampi(prev / d.width, 0, q1);  // panel of the previous one
+          for (int q = q0 + 1; q <= q1; ++q) bnd[q] = j;
+          if (j == x1 - 1)
+            for (int q = q1 + 1; q <= d.P; ++q) bnd[q] = x1;
         }
-        const int q1 = cj[u] / d.width;                                 // panel of this column
-        const int q0 = j > x0 ? clampi(pv[u] / d.width, 0, q1) : -1;  // panel of the previous one
-        for (int q = q0 + 1; q <= q1; ++q) bnd[q] = j;
-        if (j == x1 - 1)
-          for (int q = q1 + 1; q <= d.P; ++q) bnd[q] = x1;
       }
     }
-    if (__ballot(bad) && lane == 0) d.flag[id] = 0;
+    if (__ballot(bad) && lane == 0) reinterpret_cast<int*>(d.win + id)[3] = 0;
   }
+}
+
+// Inclusive sum over the wave's lanes.
+template <class T>
+__device__ __forceinline__ T wave_incl_scan(T v, int lane) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const T o = __shfl_up(v, off);
+    if (lane >= off) v += o;
+  }
+  return v;
 }
 
 __global__ __launch_bounds__(kSchedThreads) void panel_sched_kernel(Problem p) {
@@ -93,82 +114,117 @@ __global__ __launch_bounds__(kSchedThreads) void panel_sched_kernel(Problem p) {
   const int lane = lane_id();
   const int wave = t >> 6;
   constexpr int kWavesS = kSchedThreads / 64;
-  __shared__ int s_wave[kWavesS];
+  constexpr int kPer = 8;  // windows per thread per pass
+  __shared__ int s_wsum[kWavesS];
   __shared__ int s_base;
-  __shared__ long long s_w[kPanelMaxPanels];
+  __shared__ int s_id[kDevPanelSample];
+  __shared__ int s_w[kPanelMaxPanels];
+  const int P = d.P;
 
-  // 1. Compaction of the flagged ids, in id (= row) order.
+  // 1. Compaction of the flagged ids, in id (= row) order; thread t owns
+  // windows [k0 + kPer t, k0 + kPer (t + 1)).
   if (t == 0) s_base = 0;
+  for (int q = t; q < P; q += kSchedThreads) s_w[q] = 0;
   __syncthreads();
-  for (int k0 = 0; k0 < d.nwin; k0 += kSchedThreads) {
-    const int k = k0 + t;
-    const bool f = k < d.nwin && d.flag[k] == 1;
-    const unsigned long long m = __ballot(f);
-    const int before = __popcll(m & ((1ULL << lane) - 1ULL));
-    if (lane == 0) s_wave[wave] = __popcll(m);
+  for (int k0 = 0; k0 < d.nwin; k0 += kSchedThreads * kPer) {
+    bool f[kPer];
+    int cnt = 0;
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int k = k0 + t * kPer + u;
+      f[u] = k < d.nwin && reinterpret_cast<const int*>(d.win + k)[3] == 1;
+      cnt += f[u] ? 1 : 0;
+    }
+    const int incl = wave_incl_scan(cnt, lane);
+    if (lane == 63) s_wsum[wave] = incl;
     __syncthreads();
-    int off = s_base;
-    for (int v = 0; v < wave; ++v) off += s_wave[v];
-    const int i = off + before;
-    if (k < d.nwin) {
-      const bool take = f && i < d.nl_max;
-      d.pidx[k] = take ? i : -1;
-      if (take) d.list[i] = k;
+    int i = s_base + incl - cnt;
+    for (int v = 0; v < wave; ++v) i += s_wsum[v];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int k = k0 + t * kPer + u;
+      if (k < d.nwin) {
+        const bool take = f[u] && i < d.nl_max;
+        d.pidx[k] = take ? i : -1;
+        if (take) d.list[i] = k;
+      }
+      i += f[u] ? 1 : 0;
     }
     __syncthreads();
     if (t == 0) {
       int tot = 0;
-      for (int v = 0; v < kWavesS; ++v) tot += s_wave[v];
+      for (int v = 0; v < kWavesS; ++v) tot += s_wsum[v];
       s_base += tot;
     }
     __syncthreads();
   }
   const int nl = min(s_base, d.nl_max);
 
-  // 2. Panel loads from up to kDevPanelSample evenly spaced rows.
-  const int P = d.P;
+  // 2. Panel loads from ns <= kDevPanelSample evenly spaced rows: pair
+  // m = (sample m / P, panel m % P), all loads of a thread in flight at once.
   const int ns = min(nl, kDevPanelSample);
-  for (int q = t; q < P; q += kSchedThreads) s_w[q] = 0;
+  if (t < ns) s_id[t] = d.list[(int)(((long long)t * nl) / ns)];
   __syncthreads();
-  if (ns > 0) {
-    // thread t: panel q = t % P, samples t / P, t / P + stride, ...
-    const int per = kSchedThreads / P > 0 ? kSchedThreads / P : 1;
-    const int q = t % P;
-    const int s0 = t / P;
-    if (s0 < per) {
-      long long acc = 0;
-      for (int sidx = s0; sidx < ns; sidx += per) {
-        const int i = (int)(((long long)sidx * nl) / ns);
-        const int* b = d.bnd + (long long)d.list[i] * (P + 1);
-        acc += (long long)max(b[q + 1] - b[q], 0);
-      }
-      atomicAdd(reinterpret_cast<unsigned long long*>(&s_w[q]), (unsigned long long)acc);
+  constexpr int kPairs = kDevPanelSample * kPanelMaxPanels / kSchedThreads;
+  const int npairs = ns * P;
+  int b0[kPairs], b1[kPairs];
+#pragma unroll
+  for (int u = 0; u < kPairs; ++u) {
+    const int m = t + u * kSchedThreads;
+    b0[u] = b1[u] = 0;
+    if (m < npairs) {
+      const int* b = d.bnd + (long long)s_id[m / P] * (P + 1) + (m % P);
+      b0[u] = b[0];
+      b1[u] = b[1];
     }
+  }
+#pragma unroll
+  for (int u = 0; u < kPairs; ++u) {
+    const int m = t + u * kSchedThreads;
+    if (m < npairs) atomicAdd(&s_w[m % P], max(b1[u] - b0[u], 0));
   }
   __syncthreads();
 
-  // 3. Skew rule and the XCD ranges: range x ends at the last panel whose
-  // load prefix stays within x / kXcds of the total.
-  if (t == 0) {
-    long long total = 0, mx = 0;
-    for (int q = 0; q < P; ++q) {
-      total += s_w[q];
-      mx = max(mx, s_w[q]);
+  // 3. Skew rule and the XCD ranges (wave 0; lane l holds panels 4l .. 4l+3):
+  // range x ends after the leading panels whose load prefix stays within
+  // x / kXcds of the total.
+  if (wave != 0) return;
+  long long wq[4], pre[4];
+  long long local = 0, mx = 0;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int q = 4 * lane + u;
+    wq[u] = q < P ? s_w[q] : 0;
+    local += wq[u];
+    mx = max(mx, wq[u]);
+  }
+  const long long incl = wave_incl_scan(local, lane);
+  const long long total = __shfl(incl, 63);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = max(mx, __shfl_xor(mx, off));
+  long long run = incl - local;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    run += wq[u];
+    pre[u] = run;
+  }
+  const bool skewed = total > 0 && mx * P > (long long)kPanelSkewMax * total;
+  for (int x = 1; x < kXcds; ++x) {
+    int c = 0;
+    if (total > 0) {
+      const long long target = total * x / kXcds;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) c += (4 * lane + u < P && pre[u] <= target) ? 1 : 0;
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) c += __shfl_xor(c, off);
+    } else {
+      c = (int)((long long)P * x / kXcds);
     }
-    const bool skewed = total > 0 && mx * P > (long long)kPanelSkewMax * total;
+    if (lane == 0) d.sched[1 + x] = c;
+  }
+  if (lane == 0) {
     d.sched[0] = skewed ? 0 : nl;
     d.sched[1] = 0;
-    long long pre = 0;
-    int q = 0;
-    for (int x = 1; x < kXcds; ++x) {
-      if (total > 0) {
-        const long long target = total * x / kXcds;
-        while (q < P && pre + s_w[q] <= target) pre += s_w[q++];
-        d.sched[1 + x] = q;
-      } else {
-        d.sched[1 + x] = (int)((long long)P * x / kXcds);
-      }
-    }
     d.sched[1 + kXcds] = P;
   }
 }

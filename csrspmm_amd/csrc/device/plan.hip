@@ -76,7 +76,7 @@ struct csrspmm_plan_s {
   const float* vals = nullptr;
   bool use_plan = false;
   int maxlen = 0;
-  int nslots = 0, nblocks = 0;
+  int nslots = 0, mblk = kMergeBlock, nblocks = 0;
   int* d_block_start = nullptr;
   int2* d_seg_info = nullptr;
   // panelized rows
@@ -139,7 +139,8 @@ int build_rowgroup_plan(csrspmm_plan_s* p, const std::vector<int>& rp, int n_hin
   p->use_plan = ((long long)M + nnz >= kPlanMinItems) || maxlen > kLongRow;
   if (!p->use_plan) return 0;
   p->nslots = nnz / kSegLen;
-  p->nblocks = (int)(((long long)M + nnz + 1 + kMergeBlock - 1) / kMergeBlock);
+  p->mblk = merge_block(vec);
+  p->nblocks = merge_blocks(M, nnz, p->mblk);
 
   // Panelized rows: long, on a large B, with non-decreasing columns.
   // Only the float4 kernels gain: the scalar-column kernel (one 64-lane group
@@ -172,8 +173,8 @@ int build_rowgroup_plan(csrspmm_plan_s* p, const std::vector<int>& rp, int n_hin
   long long fprev = -1;
   for (int r = 0; r <= M; ++r) {
     const long long f = (long long)r + rp[r];
-    const long long b_lo = fprev < 0 ? 0 : fprev / kMergeBlock + 1;
-    const long long b_hi = std::min(f / kMergeBlock, (long long)p->nblocks - 1);
+    const long long b_lo = fprev < 0 ? 0 : fprev / p->mblk + 1;
+    const long long b_hi = std::min(f / p->mblk, (long long)p->nblocks - 1);
     for (long long b = b_lo; b <= b_hi; ++b) block_start[(size_t)b] = r;
     fprev = f;
     if (r == M) break;
@@ -309,7 +310,7 @@ int csrspmm_plan_create(int algo, int M, int K, int nnz, const int* rowptr, cons
   *out = nullptr;
   if (M < 0 || K < 0 || nnz < 0 || !rowptr || (nnz > 0 && (!colidx || !vals || K == 0)))
     return CSRSPMM_STATUS_INVALID_VALUE;
-  if ((long long)M + nnz + 1 > 0x7fffffffLL - kMergeBlock) return CSRSPMM_STATUS_NOT_SUPPORTED;
+  if ((long long)M + nnz + 1 > 0x7fffffffLL - kMergeBlockMax) return CSRSPMM_STATUS_NOT_SUPPORTED;
   const int n_eff = n_hint > 0 ? n_hint : 128;
   const int concrete = resolve_algorithm(algo, n_eff);
   if (concrete < 0) return CSRSPMM_STATUS_INVALID_VALUE;
@@ -368,6 +369,7 @@ int csrspmm_plan_spmm_f32(csrspmm_plan_t plan, int N, const float* B, long long 
   pr.plan = true;
   pr.plan_ready = true;
   pr.nslots = p->nslots;
+  pr.mblk = p->mblk;
   pr.nblocks = p->nblocks;
   pr.block_start = p->d_block_start;
   pr.seg_info = p->d_seg_info;

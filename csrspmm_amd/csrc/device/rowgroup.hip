@@ -30,6 +30,10 @@
 
 #include "common.hpp"
 
+#include <map>
+#include <mutex>
+#include <utility>
+
 namespace csrspmm_hip {
 
 namespace {
@@ -55,12 +59,11 @@ constexpr int kVec4U = CSRSPMM_VEC4_UNROLL;
 #define CSRSPMM_SEG_UNROLL 4
 #endif
 
-// Workgroups per XCD of the pieces kernel (a persistent grid: about as many
-// as the XCD's 32 CUs hold at once).
-#ifndef CSRSPMM_PIECE_BLOCKS_PER_XCD
-#define CSRSPMM_PIECE_BLOCKS_PER_XCD 256
+
+// B-row gathers in flight per lane in the pieces kernel; build-time tunable.
+#ifndef CSRSPMM_PIECE_UNROLL
+#define CSRSPMM_PIECE_UNROLL 4
 #endif
-constexpr int kPieceBlocksPerXcd = CSRSPMM_PIECE_BLOCKS_PER_XCD;
 
 __device__ __forceinline__ void wave_lds_sync() {
   // The LDS stage is private to the wave: order its writes against the
@@ -144,18 +147,24 @@ __device__ __forceinline__ void chunk_gather(const Problem& p, const Panel<VEC, 
   if constexpr (LDS) wave_lds_sync();
 }
 
-// Walks nonzeros [start, end) in chunks of G with the next chunk's (col, val)
-// prefetched, calling consume(j, v, b[T]) for each in order.
-template <int VEC, int G, int T, int U, bool LDS, class Consume>
-__device__ __forceinline__ void stream_nonzeros(const Problem& p, const Panel<VEC, G, T>& pn,
-                                                int start, int end, int gl, int gbase, int2* stage,
-                                                Consume&& consume) {
-  int cj = 0;
-  float vj = 0.0f;
-  if (start + gl < end) {
-    cj = ld_stream(p.colidx + start + gl);
-    vj = ld_stream(p.vals + start + gl);
+// Lane gl's (col, val) of the chunk of G nonzeros starting at j0 (0 past end).
+__device__ __forceinline__ void load_chunk(const Problem& p, int j0, int end, int gl, int& cj,
+                                           float& vj) {
+  cj = 0;
+  vj = 0.0f;
+  if (j0 + gl < end) {
+    cj = ld_stream(p.colidx + j0 + gl);
+    vj = ld_stream(p.vals + j0 + gl);
   }
+}
+
+// Walks nonzeros [start, end) in chunks of G with the next chunk's (col, val)
+// prefetched, calling consume(j, v, b[T]) for each in order; (cj, vj) is the
+// caller's load of the first chunk.
+template <int VEC, int G, int T, int U, bool LDS, class Consume>
+__device__ __forceinline__ void stream_nonzeros_from(const Problem& p, const Panel<VEC, G, T>& pn,
+                                                     int start, int end, int cj, float vj, int gl,
+                                                     int gbase, int2* stage, Consume&& consume) {
   for (int base = start; base < end; base += G) {
     const int jn = base + G + gl;
     int cn = 0;
@@ -169,6 +178,16 @@ __device__ __forceinline__ void stream_nonzeros(const Problem& p, const Panel<VE
     cj = cn;
     vj = vn;
   }
+}
+
+template <int VEC, int G, int T, int U, bool LDS, class Consume>
+__device__ __forceinline__ void stream_nonzeros(const Problem& p, const Panel<VEC, G, T>& pn,
+                                                int start, int end, int gl, int gbase, int2* stage,
+                                                Consume&& consume) {
+  int cj;
+  float vj;
+  load_chunk(p, start, end, gl, cj, vj);
+  stream_nonzeros_from<VEC, G, T, U, LDS>(p, pn, start, end, cj, vj, gl, gbase, stage, consume);
 }
 
 template <int VEC, int T>
@@ -225,8 +244,97 @@ __device__ __forceinline__ void stream_rows(const Problem& p, const Panel<VEC, G
   }
 }
 
+// Pieces of this call's column panels, run by the first blocks of the main
+// launch.  Pieces block b runs on XCD b mod kXcds and shares with the other
+// pieces blocks of that XCD the pieces of its panel range [qa, qb): piece i
+// is (panel qa + i / nl, panelized row i mod nl), the nonzeros of that row
+// whose columns fall in the panel, summed into the partial (row, panel).
+// Pieces are dealt group-strided in panel order, so the groups of an XCD
+// work within a few panels at a time and gather from a band of B that stays
+// in that XCD's L2.  The pieces blocks are as many as the GPU holds at once
+// and come first in the grid; the short-row and segment blocks behind them
+// take over each slot as its pieces run out, which absorbs the uneven finish
+// of static dealing.
 template <int VEC, int G, int T, int U, bool LDS>
-__global__ __launch_bounds__(kWaves * 64) void rowgroup_kernel(Problem p, int seg_blocks) {
+__device__ __forceinline__ void pieces_body(const Problem& p, int block, int nblocks, int gl,
+                                            int gbase, int gid, int2* stage) {
+  using VT = typename Vec<VEC>::T;
+  constexpr int GPB = kWaves * (64 / G);
+  constexpr int PW = G * VEC * T;
+  constexpr int UP = CSRSPMM_PIECE_UNROLL < G ? CSRSPMM_PIECE_UNROLL : G;
+  const DevPanels& d = p.dp;
+  const int nl = d.sched[0];
+  if (nl <= 0) return;
+  const int x = block % kXcds;
+  const int qa = d.sched[1 + x];
+  const unsigned n = (unsigned)max(d.sched[2 + x] - qa, 0) * (unsigned)nl;
+  const unsigned stride = (unsigned)((nblocks / kXcds) * GPB);
+  unsigned i = (unsigned)((block / kXcds) * GPB + gid);
+  if (i >= n) return;
+  const int P1 = d.P + 1;
+  auto bounds = [&](unsigned k, int id, int& a, int& e) {
+    const int* b = d.bnd + (long long)id * P1 + (qa + (int)(k / (unsigned)nl));
+    a = min(max(b[0], 0), p.nnz);  // a malformed CSR cannot send the loads out of A
+    e = min(max(b[1], a), p.nnz);
+  };
+  // Software pipeline: while piece i is summed, the bounds of piece i + stride
+  // and the row id of piece i + 2 stride are in flight, and the first chunk
+  // of piece i + stride is loaded before piece i's partial is stored.
+  int a, e;
+  bounds(i, d.list[i % (unsigned)nl], a, e);
+  int id1 = i + stride < n ? d.list[(i + stride) % (unsigned)nl] : 0;
+  int cj;
+  float vj;
+  load_chunk(p, a, e, gl, cj, vj);
+  for (;;) {
+    const unsigned i1 = i + stride;
+    int a1 = 0, e1 = 0, id2 = 0;
+    if (i1 < n) {
+      bounds(i1, id1, a1, e1);
+      if (i1 + stride < n) id2 = d.list[(i1 + stride) % (unsigned)nl];
+    }
+    const int q = qa + (int)(i / (unsigned)nl);
+    float* prow = d.part + ((long long)(i % (unsigned)nl) * d.P + q) * p.ldp;
+    const Panel<VEC, G, T> pn0(p, 0, gl);
+    VT acc[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) acc[t] = Vec<VEC>::zero();
+    stream_nonzeros_from<VEC, G, T, UP, LDS>(p, pn0, a, e, cj, vj, gl, gbase, stage,
+                                             [&](int, float v, const VT(&bv)[T]) {
+#pragma unroll
+                                               for (int t = 0; t < T; ++t) acc[t] = fma_v(v, bv[t], acc[t]);
+                                             });
+    if (i1 < n) load_chunk(p, a1, e1, gl, cj, vj);
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      if (pn0.cval[t]) *reinterpret_cast<VT*>(prow + pn0.col[t]) = acc[t];
+    }
+    // columns beyond the first PW (N > G * VEC * T): the rest of the piece, plainly
+    for (int c0 = PW; c0 < p.N; c0 += PW) {
+      const Panel<VEC, G, T> pn(p, c0, gl);
+#pragma unroll
+      for (int t = 0; t < T; ++t) acc[t] = Vec<VEC>::zero();
+      stream_nonzeros<VEC, G, T, UP, LDS>(p, pn, a, e, gl, gbase, stage,
+                                          [&](int, float v, const VT(&bv)[T]) {
+#pragma unroll
+                                            for (int t = 0; t < T; ++t) acc[t] = fma_v(v, bv[t], acc[t]);
+                                          });
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        if (pn.cval[t]) *reinterpret_cast<VT*>(prow + pn.col[t]) = acc[t];
+      }
+    }
+    if (i1 >= n) break;
+    i = i1;
+    a = a1;
+    e = e1;
+    id1 = id2;
+  }
+}
+
+template <int VEC, int G, int T, int U, bool LDS>
+__global__ __launch_bounds__(kWaves * 64) void rowgroup_kernel(Problem p, int piece_blocks,
+                                                                int seg_blocks) {
   using VT = typename Vec<VEC>::T;
   constexpr int GPW = 64 / G;        // groups per wave
   constexpr int GPB = kWaves * GPW;  // groups per block
@@ -240,11 +348,18 @@ __global__ __launch_bounds__(kWaves * 64) void rowgroup_kernel(Problem p, int se
   __shared__ int2 stage_all[LDS ? kWaves * 64 : 1];
   int2* stage = stage_all + (LDS ? wave * 64 : 0);
 
-  if ((int)blockIdx.x < seg_blocks) {
+  if constexpr (VEC == 4) {  // column panels are built for float4 columns only
+    if ((int)blockIdx.x < piece_blocks) {
+      pieces_body<VEC, G, T, U, LDS>(p, (int)blockIdx.x, piece_blocks, gl, gbase, gid, stage);
+      return;
+    }
+  }
+  const int bid = (int)blockIdx.x - piece_blocks;
+  if (bid < seg_blocks) {
     // Long-row segments, one slot per group (grid-strided if the segment
     // blocks are capped).
     constexpr int US = CSRSPMM_SEG_UNROLL > U ? (CSRSPMM_SEG_UNROLL < G ? CSRSPMM_SEG_UNROLL : G) : U;
-    for (int s = blockIdx.x * GPB + gid; s < p.nslots; s += seg_blocks * GPB) {
+    for (int s = bid * GPB + gid; s < p.nslots; s += seg_blocks * GPB) {
       const int2 si = p.seg_info[s];
       if (si.x < 0 || si.x >= p.M) continue;  // unused slot
       const int rs = p.rowptr[si.x];
@@ -278,7 +393,7 @@ __global__ __launch_bounds__(kWaves * 64) void rowgroup_kernel(Problem p, int se
     return;
   }
 
-  const int unit = ((int)blockIdx.x - seg_blocks) * GPB + gid;
+  const int unit = (bid - seg_blocks) * GPB + gid;
   if (p.plan) {
     // One merge block of short rows.
     if (unit >= p.nblocks) return;
@@ -310,68 +425,6 @@ __global__ __launch_bounds__(kWaves * 64) void rowgroup_kernel(Problem p, int se
   }
 }
 
-// Pieces of this call's column panels.  Workgroup b runs on XCD b mod kXcds
-// and shares with the other workgroups of that XCD the pieces of its panel
-// range [qa, qb): piece i is (panel qa + i / nl, panelized row i mod nl), the
-// nonzeros of that row whose columns fall in the panel, summed into the
-// partial (row, panel).  Pieces are dealt group-strided in panel order, so
-// the groups of an XCD work within a few panels at a time and gather from a
-// band of B that stays in that XCD's L2.  The grid is fixed; every group
-// leaves its loop when the pieces of its range run out.
-template <int VEC, int G, int T, int U, bool LDS>
-__global__ __launch_bounds__(kWaves * 64) void panel_pieces_kernel(Problem p) {
-  using VT = typename Vec<VEC>::T;
-  constexpr int GPW = 64 / G;
-  constexpr int GPB = kWaves * GPW;
-  constexpr int PW = G * VEC * T;
-  constexpr int US = CSRSPMM_SEG_UNROLL > U ? (CSRSPMM_SEG_UNROLL < G ? CSRSPMM_SEG_UNROLL : G) : U;
-  const DevPanels& d = p.dp;
-  const int nl = d.sched[0];
-  if (nl <= 0) return;
-  const int lane = lane_id();
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int gl = lane & (G - 1);
-  const int gbase = lane & ~(G - 1);
-  const int gid = wave * GPW + lane / G;
-  __shared__ int2 stage_all[LDS ? kWaves * 64 : 1];
-  int2* stage = stage_all + (LDS ? wave * 64 : 0);
-
-  const int x = (int)blockIdx.x % kXcds;
-  const int jb = (int)blockIdx.x / kXcds;
-  const int nb = (int)gridDim.x / kXcds;
-  const int qa = d.sched[1 + x];
-  const int qb = d.sched[2 + x];
-  const unsigned npieces = (unsigned)max(qb - qa, 0) * (unsigned)nl;
-  for (unsigned i = (unsigned)(jb * GPB + gid); i < npieces; i += (unsigned)(nb * GPB)) {
-    const int q = qa + (int)(i / (unsigned)nl);
-    const int ri = (int)(i % (unsigned)nl);
-    const int id = d.list[ri];
-    const int r = d.win_row[id];
-    if (r < 0 || r >= p.M) continue;  // only for a malformed rowptr
-    const int x0 = clamp_nnz(p.rowptr[r], p.nnz);
-    const int x1 = max(x0, clamp_nnz(p.rowptr[r + 1], p.nnz));
-    const int* b = d.bnd + (long long)id * (d.P + 1);
-    const int a = min(max(b[q], x0), x1);
-    const int e = min(max(b[q + 1], a), x1);
-    float* prow = d.part + ((long long)ri * d.P + q) * p.ldp;
-    for (int c0 = 0; c0 < p.N; c0 += PW) {
-      const Panel<VEC, G, T> pn(p, c0, gl);
-      VT acc[T];
-#pragma unroll
-      for (int t = 0; t < T; ++t) acc[t] = Vec<VEC>::zero();
-      stream_nonzeros<VEC, G, T, US, LDS>(p, pn, a, e, gl, gbase, stage,
-                                          [&](int, float v, const VT(&bv)[T]) {
-#pragma unroll
-                                            for (int t = 0; t < T; ++t) acc[t] = fma_v(v, bv[t], acc[t]);
-                                          });
-#pragma unroll
-      for (int t = 0; t < T; ++t) {
-        if (pn.cval[t]) *reinterpret_cast<VT*>(prow + pn.col[t]) = acc[t];
-      }
-    }
-  }
-}
-
 // One thread per row r in [0, M]: the merge-block starts that fall on r, and
 // the segment slots r owns.  Every entry the main kernel reads is written
 // here on each call, from rowptr alone (no counters to reset, no atomics).
@@ -379,11 +432,11 @@ __global__ __launch_bounds__(256) void plan_kernel(Problem p) {
   const int stride = gridDim.x * blockDim.x;
   for (int r = blockIdx.x * blockDim.x + threadIdx.x; r <= p.M; r += stride) {
     const int x0 = clamp_nnz(p.rowptr[r], p.nnz);
-    // merge blocks b with F(r-1) < b*kMergeBlock <= F(r) start at row r
+    // merge blocks b with F(r-1) < b*mblk <= F(r) start at row r
     const long long F = (long long)r + x0;
     const long long Fprev = r > 0 ? (long long)(r - 1) + clamp_nnz(p.rowptr[r - 1], p.nnz) : -1;
-    const long long b_lo = Fprev < 0 ? 0 : Fprev / kMergeBlock + 1;
-    const long long b_hi = min(F / kMergeBlock, (long long)p.nblocks - 1);
+    const long long b_lo = Fprev < 0 ? 0 : Fprev / p.mblk + 1;
+    const long long b_hi = min(F / p.mblk, (long long)p.nblocks - 1);
     for (long long b = b_lo; b <= b_hi; ++b) p.block_start[b] = r;
     if (r == p.M) {
       p.block_start[p.nblocks] = p.M;
@@ -402,10 +455,8 @@ __global__ __launch_bounds__(256) void plan_kernel(Problem p) {
       // first of them is the row's id when the row is long
       const int w0 = (x0 + kPanelMinLen - 1) / kPanelMinLen;
       const int w1 = min((x1 + kPanelMinLen - 1) / kPanelMinLen, p.dp.nwin);
-      for (int w = w0; w < w1; ++w) {
-        p.dp.win_row[w] = r;
-        p.dp.flag[w] = (w == w0 && len >= kPanelMinLen) ? 1 : 0;
-      }
+      for (int w = w0; w < w1; ++w)
+        p.dp.win[w] = make_int4(r, x0, x1, (w == w0 && len >= kPanelMinLen) ? 1 : 0);
     }
   }
 }
@@ -509,7 +560,7 @@ __global__ __launch_bounds__(kWaves * 64) void combine_kernel(Problem p, int sca
   if (p.dp.P > 0) {
     // this call's panelized row i: partials (i, 0 .. P-1), in column order
     if (i >= p.dp.sched[0]) return;
-    row = p.dp.win_row[p.dp.list[i]];
+    row = p.dp.win[p.dp.list[i]].x;
     if (row < 0 || row >= p.M) return;  // only for a malformed rowptr
     npc = p.dp.P;
     pieces = nullptr;
@@ -556,6 +607,27 @@ void launch_combine(const Problem& p, hipStream_t s) {
   }
 }
 
+// Blocks of 256 threads of `kernel` the current device holds at once (CUs x
+// blocks per CU), a multiple of kXcds; cached per kernel and device.
+int resident_blocks(const void* kernel) {
+  static std::mutex mu;
+  static std::map<std::pair<const void*, int>, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find({kernel, dev});
+  if (it != cache.end()) return it->second;
+  int per_cu = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kWaves * 64, 0) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  const int n = std::max(kXcds, (per_cu * cus) / kXcds * kXcds);
+  cache[{kernel, dev}] = n;
+  return n;
+}
+
 template <int VEC, int G, int T, int U, bool LDS>
 hipError_t launch_rg(const Problem& p, hipStream_t s) {
   constexpr int GPB = kWaves * (64 / G);
@@ -563,17 +635,15 @@ hipError_t launch_rg(const Problem& p, hipStream_t s) {
   const int unit_blocks = div_up_host(units, GPB);
   const int seg_blocks =
       (p.plan && p.nslots > 0) ? std::min(kSegBlocksMax, div_up_host(p.nslots, GPB)) : 0;
-  const long long blocks = (long long)unit_blocks + seg_blocks;
-  if constexpr (VEC == 4) {  // panels are built for float4 columns only
-    if (p.dp.P > 0) {
-      // the pieces of panelized rows first, alone, so nothing else evicts their bands
-      hipLaunchKernelGGL((panel_pieces_kernel<VEC, G, T, U, LDS>), dim3(kXcds * kPieceBlocksPerXcd),
-                         dim3(kWaves * 64), 0, s, p);
-    }
+  int piece_blocks = 0;
+  if (VEC == 4 && p.dp.P > 0) {
+    piece_blocks = resident_blocks(reinterpret_cast<const void*>(rowgroup_kernel<VEC, G, T, U, LDS>));
+    if (piece_blocks <= 0) return hipErrorInvalidDeviceFunction;
   }
-  if (blocks == 0) return hipGetLastError();
+  const long long blocks = (long long)piece_blocks + unit_blocks + seg_blocks;
+  if (blocks == 0) return hipSuccess;
   hipLaunchKernelGGL((rowgroup_kernel<VEC, G, T, U, LDS>), dim3((unsigned)blocks), dim3(kWaves * 64),
-                     0, s, p, seg_blocks);
+                     0, s, p, piece_blocks, seg_blocks);
   return hipGetLastError();
 }
 

@@ -50,10 +50,22 @@ __host__ __device__ inline int seg_begin(int len, int nseg, int k) {
 // the rows r with F(r) in [b*kMergeBlock, (b+1)*kMergeBlock), so every block
 // carries at most kMergeBlock (rows + nonzeros) of short-row work plus one
 // row's tail, and runs of empty rows are spread like nonzeros.
+// The block is smaller for float4 columns (measured on MI355X: 64 for
+// float4, whose groups are narrower and more per wave; 128 for scalar ones).
 #ifndef CSRSPMM_MERGE_BLOCK
 #define CSRSPMM_MERGE_BLOCK 128
 #endif
+#ifndef CSRSPMM_MERGE_BLOCK_VEC4
+#define CSRSPMM_MERGE_BLOCK_VEC4 64
+#endif
 constexpr int kMergeBlock = CSRSPMM_MERGE_BLOCK;
+constexpr int kMergeBlockVec4 = CSRSPMM_MERGE_BLOCK_VEC4;
+constexpr int kMergeBlockMin = kMergeBlock < kMergeBlockVec4 ? kMergeBlock : kMergeBlockVec4;
+constexpr int kMergeBlockMax = kMergeBlock > kMergeBlockVec4 ? kMergeBlock : kMergeBlockVec4;
+inline int merge_block(int vec) { return vec == 4 ? kMergeBlockVec4 : kMergeBlock; }
+inline int merge_blocks(int M, int nnz, int mblk) {
+  return (int)(((long long)M + nnz + 1 + mblk - 1) / mblk);
+}
 
 // Below this many (rows + nonzeros) the plan is skipped and each row is
 // processed whole by one group (one launch instead of three).
@@ -74,7 +86,7 @@ constexpr int kXcds = 8;
 #define CSRSPMM_PANEL_MIN_LEN 2048
 #endif
 #ifndef CSRSPMM_PANEL_BAND_KB
-#define CSRSPMM_PANEL_BAND_KB 512
+#define CSRSPMM_PANEL_BAND_KB 1024
 #endif
 constexpr int kPanelMinLen = CSRSPMM_PANEL_MIN_LEN;
 constexpr long long kPanelBandBytes = (long long)CSRSPMM_PANEL_BAND_KB * 1024;
@@ -104,8 +116,9 @@ struct DevPanels {
   int width;       // columns per panel, ceil(K / P)
   int nwin;        // windows, ceil(nnz / kPanelMinLen)
   int nl_max;      // panelized rows at most (rows of the partial buffer)
-  int* win_row;    // [nwin] the row holding position w * kPanelMinLen
-  int* flag;       // [nwin] 1: w = id(r) of a long row whose columns are sorted and in range
+  int4* win;       // [nwin] (r, rowptr[r], rowptr[r+1], flag) for the row r holding position
+                   // w * kPanelMinLen; flag 1: w = id(r) of a long row whose columns are
+                   // sorted and in range
   int* pidx;       // [nwin] compact index of the panelized row with id w, else -1
   int* list;       // [nl_max] ids of the panelized rows, in row order
   int* bnd;        // [nwin][P + 1] absolute position where panel q starts in the row with id w
@@ -136,6 +149,7 @@ struct Problem {
   // plan == false: every row is processed whole by its own group.
   bool plan;
   int nslots;         // nnz / kSegLen
+  int mblk;           // merge block size (rows + nonzeros)
   int nblocks;        // merge blocks
   int* block_start;   // nblocks + 1 entries: first row of each merge block, then M
   int2* seg_info;     // per slot: (row, segment index) or (-1, 0) for an unused slot
@@ -160,7 +174,7 @@ struct Problem {
 // the per-call panel tables and partial buffer after the base sections.
 struct WorkspaceLayout {
   size_t block_start_off, seg_info_off, partials_off, base_total;
-  size_t win_row_off, flag_off, pidx_off, list_off, bnd_off, sched_off, part_off, total;
+  size_t win_off, pidx_off, list_off, bnd_off, sched_off, part_off, total;
   int nslots, nblocks;
   long long ldp;
   int P, width, nwin, nl_max;
@@ -171,8 +185,9 @@ WorkspaceLayout workspace_layout(int M, int K, int N, int nnz, int P);
 // the plan on, and a row of kPanelMinLen nonzeros possible under the hint.
 int per_call_panels(int vec, bool plan, int K, int N, int nnz, int hint);
 
-// Bind the plan pointers of p into a workspace base pointer.
-void bind_workspace(Problem& p, void* ws, const WorkspaceLayout& L);
+// Bind the plan pointers of p into a workspace base pointer; merge blocks of
+// mblk (the layout holds block starts for any merge block size).
+void bind_workspace(Problem& p, void* ws, const WorkspaceLayout& L, int mblk);
 
 // Shared by the per-call C ABI and stored plans (capi.hip).
 int resolve_algorithm(int algo, int N);  // CSRSPMM_ALGO_AUTO -> a concrete variant; -1 if invalid
