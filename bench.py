@@ -8,8 +8,10 @@ two torch.cuda.synchronize() calls, timed with HIP events on the launch
 stream.  Prints ONE JSON line:
   value      GFLOPS = 2*nnz*N / (ms_per_step) for the headline variant
              (Auto by default: the variant the library picks from N)
-  roofline   achieved gather-model GB/s of the main kernel (HIP event pair
-             around it, csrspmm_timing_*) against 8 TB/s
+  roofline   achieved gather-model GB/s of one SpMM call on the GPU (a HIP
+             event pair around all of the call's launches, recorded by the
+             library on the launch stream, csrspmm_timing_*) against 8 TB/s;
+             traffic = measured HBM bytes per call from profiles/traffic.json
   variants   the same figures for every variant on the same config
   plan       the same figures for a stored plan (csrspmm_plan_*, Auto by
              default) built once outside the timed region, with its build
@@ -210,9 +212,9 @@ def main():
     if os.path.exists(args.traffic_file):
         with open(args.traffic_file) as f:
             tr = json.load(f)
-        key = f"{cfg.name}/{resolved}"
+        key = f"{cfg.name}/{args.algo}"
         if key in tr:
-            traffic = tr[key]["bytes_per_launch"]
+            traffic = tr[key]["bytes_per_call"]
 
     cpu = None
     if args.cpu_seconds > 0:
