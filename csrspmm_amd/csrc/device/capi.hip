@@ -32,8 +32,11 @@ WorkspaceLayout workspace_layout(int M, int K, int N, int nnz, int P) {
   off = align256(off + (size_t)L.nslots * (size_t)L.ldp * sizeof(float));
   L.base_total = off;
   if (P > 0 && K > 0) {
-    L.P = P;
-    L.width = (int)(((long long)K + P - 1) / P);
+    const long long w = ((long long)K + P - 1) / P;
+    L.wshift = 0;
+    while ((1LL << L.wshift) < w) ++L.wshift;
+    L.P = (int)(((long long)K + (1LL << L.wshift) - 1) >> L.wshift);
+    P = L.P;
     L.nwin = (int)(((long long)nnz + kPanelMinLen - 1) / kPanelMinLen);
     const long long per_row = (long long)P * L.ldp * (long long)sizeof(float);
     L.nl_max = (int)std::min<long long>(L.nwin, std::max<long long>(1, kDevPanelPartialBudget / per_row));
@@ -67,7 +70,7 @@ void bind_workspace(Problem& p, void* ws, const WorkspaceLayout& L, int mblk) {
   p.dp = DevPanels{};
   if (L.P > 0) {
     p.dp.P = L.P;
-    p.dp.width = L.width;
+    p.dp.wshift = L.wshift;
     p.dp.nwin = L.nwin;
     p.dp.nl_max = L.nl_max;
     p.dp.win = reinterpret_cast<int4*>(b + L.win_off);

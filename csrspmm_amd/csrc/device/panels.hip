@@ -85,8 +85,8 @@ __global__ __launch_bounds__(256) void panel_window_kernel(Problem p) {
         if (cj < 0 || cj >= p.K || (!first && prev > cj)) {
           bad = true;
         } else {
-          const int q1 = cj / d.width;                                // panel of this column
-          const int q0 = first ? -1 : clampi(prev / d.width, 0, q1);  // panel of the previous one
+          const int q1 = cj >> d.wshift;                                // panel of this column
+          const int q0 = first ? -1 : clampi(prev >> d.wshift, 0, q1);  // panel of the previous one
           for (int q = q0 + 1; q <= q1; ++q) bnd[q] = j;
           if (j == x1 - 1)
             for (int q = q1 + 1; q <= d.P; ++q) bnd[q] = x1;

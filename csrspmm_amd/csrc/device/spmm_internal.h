@@ -83,7 +83,7 @@ constexpr int kXcds = 8;
 // plans build the schedule on the host (plan.hip); the per-call path builds
 // it on the device (panels.hip).
 #ifndef CSRSPMM_PANEL_MIN_LEN
-#define CSRSPMM_PANEL_MIN_LEN 2048
+#define CSRSPMM_PANEL_MIN_LEN 1024
 #endif
 #ifndef CSRSPMM_PANEL_BAND_KB
 #define CSRSPMM_PANEL_BAND_KB 1024
@@ -112,8 +112,9 @@ inline int panel_count(int K, int N) {
 constexpr long long kDevPanelPartialBudget = 256LL << 20;  // bytes of piece partials, at most
 constexpr int kDevPanelSample = 64;  // rows sampled for the panel loads
 struct DevPanels {
-  int P;           // panels; 0 = off
-  int width;       // columns per panel, ceil(K / P)
+  int P;           // panels, ceil(K / 2^wshift) <= panel_count(K, N); 0 = off
+  int wshift;      // columns per panel = 2^wshift: ceil(K / panel_count) rounded up to a power
+                   // of two, so a column's panel is a shift
   int nwin;        // windows, ceil(nnz / kPanelMinLen)
   int nl_max;      // panelized rows at most (rows of the partial buffer)
   int4* win;       // [nwin] (r, rowptr[r], rowptr[r+1], flag) for the row r holding position
@@ -177,7 +178,7 @@ struct WorkspaceLayout {
   size_t win_off, pidx_off, list_off, bnd_off, sched_off, part_off, total;
   int nslots, nblocks;
   long long ldp;
-  int P, width, nwin, nl_max;
+  int P, wshift, nwin, nl_max;
 };
 WorkspaceLayout workspace_layout(int M, int K, int N, int nnz, int P);
 

@@ -85,9 +85,9 @@ int csrspmm_resolve_algorithm(int algo, int N);
 size_t csrspmm_workspace_bytes(int algo, int M, int N, int nnz);
 
 /* As csrspmm_workspace_bytes, plus the per-call column-panel tables and
- * partial sums that float4 variants use for rows of >= 2048 nonzeros when B
+ * partial sums that float4 variants use for rows of >= 1024 nonzeros when B
  * (K x N fp32) is >= 16 MiB and N <= 256 (at most 256 MiB of partials).  A
- * max_row_nnz_hint in [0, 2048) (or -1: unknown) tells that no such row
+ * max_row_nnz_hint in [0, 1024) tells that no such row exists (-1: unknown)
  * exists.  csrspmm_spmm_f32_ex given a workspace of at least
  * csrspmm_workspace_bytes but less than this size runs without panels. */
 size_t csrspmm_workspace_bytes_ex(int algo, int M, int K, int N, int nnz, int max_row_nnz_hint);
@@ -153,7 +153,7 @@ int csrspmm_spmm_f32_ex(int algo, int M, int K, int N, int nnz,
  * keeps on the device:
  *  - the merge-block starts and long-row segment slots (no per-call plan
  *    kernel);
- *  - for rows of >= 2048 nonzeros with sorted columns when K*N*4 >= 16 MiB, a
+ *  - for rows of >= 1024 nonzeros with sorted columns when K*N*4 >= 16 MiB, a
  *    column-panel copy of the row pieces, laid out so that each of the 8 XCDs
  *    streams its own panels in order and keeps the gathered B band in its L2;
  *  - partial-sum buffers for n_hint columns (grown on a call with larger N).

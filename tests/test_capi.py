@@ -148,12 +148,13 @@ def test_csr_tools_argument_errors_without_device():
 
 def test_workspace_bytes_ex_panels():
     """The panel tables are reserved only for float4 variants on a B of
-    >= 16 MiB when a row of >= 2048 nonzeros is possible under the hint."""
+    >= 16 MiB when a row of >= 1024 nonzeros is possible under the hint."""
     lib = capi.hip()
     a = capi.ALGO["WarpPerRowSmemFp4"]
     M, K, N, nnz = 262144, 262144, 128, 8453223
     base = lib.csrspmm_workspace_bytes(a, M, N, nnz)
-    assert lib.csrspmm_workspace_bytes_ex(a, M, K, N, nnz, 2047) == base
+    assert lib.csrspmm_workspace_bytes_ex(a, M, K, N, nnz, 1023) == base
+    assert lib.csrspmm_workspace_bytes_ex(a, M, K, N, nnz, 1024) > base
     full = lib.csrspmm_workspace_bytes_ex(a, M, K, N, nnz, -1)
     assert full == lib.csrspmm_workspace_bytes_ex(a, M, K, N, nnz, 16384) > base
     # partials at most 256 MiB, plus tables of a few MiB

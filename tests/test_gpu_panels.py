@@ -1,7 +1,7 @@
 """GPU parity of the per-call column panels.
 
 With float4 columns (WarpPerRowFp4 / WarpPerRowSmemFp4 / Auto at N >= 128),
-a B of at least 16 MiB and N <= 256, every SpMM call cuts rows of >= 2048
+a B of at least 16 MiB and N <= 256, every SpMM call cuts rows of >= 1024
 nonzeros with sorted columns at column-panel boundaries on the device, sums
 the pieces panel by panel (each XCD walking its own panels) and adds a
 row's pieces in column order.  These tests put such rows next to the cases
@@ -47,7 +47,8 @@ def csr_from_lengths(lens, K, seed, narrow=None, unsorted_rows=()):
 def mixed_lengths(seed, M=3000):
     rng = np.random.default_rng(seed)
     lens = rng.integers(0, 40, size=M)
-    special = [2047, 2048, 2049, 3000, 4096, 5000, 20000, 256, 257, 511, 512, 767, 768, 0, 1, 16384]
+    special = [1023, 1024, 1025, 2047, 2048, 2049, 3000, 4096, 5000, 20000, 256, 257, 511, 512, 767,
+               768, 0, 1, 16384]
     pos = rng.choice(M, size=len(special), replace=False)
     lens[pos] = special
     lens[-1] = 6000  # a long row at the very end
