@@ -67,6 +67,7 @@ void bind_workspace(Problem& p, void* ws, const WorkspaceLayout& L, int mblk) {
   p.nslots = L.nslots;
   p.mblk = mblk;
   p.nblocks = merge_blocks(p.M, p.nnz, mblk);
+
   p.dp = DevPanels{};
   if (L.P > 0) {
     p.dp.P = L.P;
@@ -233,7 +234,10 @@ int spmm_impl(int algo_in, int M, int K, int N, int nnz, const int* rowptr, cons
   p.plan = wants_plan(algo, M, nnz, hint);
   if (p.plan) {
     const int vec = vector_width(algo, p);
-    const int P = per_call_panels(vec, true, K, N, nnz, hint);
+    int P = per_call_panels(vec, true, K, N, nnz, hint);
+    p.sw = slice_width(K, N, P > 0);
+    p.slice_launch = slice_launches(M, nnz);
+    if (p.sw > 0) P = 0;  // a sliced call gathers band by band instead
     WorkspaceLayout L = workspace_layout(M, K, N, nnz, P);
     if (owned) {
       st = owned_workspace(stream, L.total, &ws);
@@ -392,7 +396,8 @@ size_t csrspmm_workspace_bytes_ex(int algo, int M, int K, int N, int nnz, int ma
   // float4 columns as far as the shape tells (pointer alignment is checked per call)
   const bool fp4 = (algo == CSRSPMM_ALGO_WARP_PER_ROW_FP4 || algo == CSRSPMM_ALGO_WARP_PER_ROW_SMEM_FP4) &&
                    N % 4 == 0;
-  const int P = per_call_panels(fp4 ? 4 : 1, true, K, N, nnz, max_row_nnz_hint);
+  int P = per_call_panels(fp4 ? 4 : 1, true, K, N, nnz, max_row_nnz_hint);
+  if (slice_width(K, N, P > 0) > 0) P = 0;
   return workspace_layout(M, K, N, nnz, P).total;
 }
 

@@ -376,6 +376,9 @@ int csrspmm_plan_spmm_f32(csrspmm_plan_t plan, int N, const float* B, long long 
   pr.partials = p->d_partials;
   pr.ldp = p->ldp_cap;
   pr.npan = p->npan;
+  // a plan with panelized rows keeps them; otherwise large B are sliced by columns
+  pr.sw = p->npan > 0 ? 0 : slice_width(p->K, N, false);
+  pr.slice_launch = slice_launches(p->M, p->nnz);
   pr.pan_rows = p->d_pan_rows;
   pr.pan_ptr = p->d_pan_ptr;
   pr.pan_piece = p->d_pan_piece;
@@ -386,6 +389,7 @@ int csrspmm_plan_spmm_f32(csrspmm_plan_t plan, int N, const float* B, long long 
   if (p->npan > 0) {
     // the pieces of panelized rows, alone first so nothing else evicts their band
     Problem d = pr;
+    d.sw = 0;
     d.M = p->npieces;
     d.rowptr = p->d_drowptr;
     d.colidx = p->d_dcolidx;

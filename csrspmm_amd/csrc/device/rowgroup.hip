@@ -91,11 +91,11 @@ struct Panel {
   const float* bcol[T];
   bool cval[T];
   int col[T];
-  __device__ __forceinline__ Panel(const Problem& p, int c0, int gl) {
+  __device__ __forceinline__ Panel(const Problem& p, int c0, int gl, int climit) {
 #pragma unroll
     for (int t = 0; t < T; ++t) {
       col[t] = c0 + (gl + G * t) * VEC;
-      cval[t] = col[t] < p.N;  // VEC == 4 requires N % 4 == 0 (host-checked)
+      cval[t] = col[t] < climit;  // VEC == 4 requires N % 4 == 0 (host-checked)
       bcol[t] = p.B + col[t];
     }
   }
@@ -295,7 +295,7 @@ __device__ __forceinline__ void pieces_body(const Problem& p, int block, int nbl
     }
     const int q = qa + (int)(i / (unsigned)nl);
     float* prow = d.part + ((long long)(i % (unsigned)nl) * d.P + q) * p.ldp;
-    const Panel<VEC, G, T> pn0(p, 0, gl);
+    const Panel<VEC, G, T> pn0(p, 0, gl, p.N);
     VT acc[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) acc[t] = Vec<VEC>::zero();
@@ -311,7 +311,7 @@ __device__ __forceinline__ void pieces_body(const Problem& p, int block, int nbl
     }
     // columns beyond the first PW (N > G * VEC * T): the rest of the piece, plainly
     for (int c0 = PW; c0 < p.N; c0 += PW) {
-      const Panel<VEC, G, T> pn(p, c0, gl);
+      const Panel<VEC, G, T> pn(p, c0, gl, p.N);
 #pragma unroll
       for (int t = 0; t < T; ++t) acc[t] = Vec<VEC>::zero();
       stream_nonzeros<VEC, G, T, UP, LDS>(p, pn, a, e, gl, gbase, stage,
@@ -332,29 +332,15 @@ __device__ __forceinline__ void pieces_body(const Problem& p, int block, int nbl
   }
 }
 
+// One block's share of the main launch, over the columns [c_lo, c_hi):
+// block bid < seg_blocks takes long-row segment slots, the others merge
+// blocks of short rows (or, without a plan, rows).
 template <int VEC, int G, int T, int U, bool LDS>
-__global__ __launch_bounds__(kWaves * 64) void rowgroup_kernel(Problem p, int piece_blocks,
-                                                                int seg_blocks) {
+__device__ __forceinline__ void rowgroup_block(const Problem& p, int bid, int seg_blocks, int c_lo,
+                                               int c_hi, int gl, int gbase, int gid, int2* stage) {
   using VT = typename Vec<VEC>::T;
-  constexpr int GPW = 64 / G;        // groups per wave
-  constexpr int GPB = kWaves * GPW;  // groups per block
-  constexpr int PW = G * VEC * T;    // columns per panel
-  const int lane = lane_id();
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int gl = lane & (G - 1);
-  const int gbase = lane & ~(G - 1);
-  const int gid = wave * GPW + lane / G;  // group index within block
-
-  __shared__ int2 stage_all[LDS ? kWaves * 64 : 1];
-  int2* stage = stage_all + (LDS ? wave * 64 : 0);
-
-  if constexpr (VEC == 4) {  // column panels are built for float4 columns only
-    if ((int)blockIdx.x < piece_blocks) {
-      pieces_body<VEC, G, T, U, LDS>(p, (int)blockIdx.x, piece_blocks, gl, gbase, gid, stage);
-      return;
-    }
-  }
-  const int bid = (int)blockIdx.x - piece_blocks;
+  constexpr int GPB = kWaves * (64 / G);
+  constexpr int PW = G * VEC * T;
   if (bid < seg_blocks) {
     // Long-row segments, one slot per group (grid-strided if the segment
     // blocks are capped).
@@ -370,8 +356,8 @@ __global__ __launch_bounds__(kWaves * 64) void rowgroup_kernel(Problem p, int pi
       const int start = rs + seg_begin(len, nseg, si.y);
       const int end = rs + seg_begin(len, nseg, si.y + 1);
       float* prow = p.partials + (long long)s * p.ldp;
-      for (int c0 = 0; c0 < p.N; c0 += PW) {
-        const Panel<VEC, G, T> pn(p, c0, gl);
+      for (int c0 = c_lo; c0 < c_hi; c0 += PW) {
+        const Panel<VEC, G, T> pn(p, c0, gl, c_hi);
         VT acc[T];
 #pragma unroll
         for (int t = 0; t < T; ++t) acc[t] = Vec<VEC>::zero();
@@ -399,8 +385,8 @@ __global__ __launch_bounds__(kWaves * 64) void rowgroup_kernel(Problem p, int pi
     if (unit >= p.nblocks) return;
     const int rs = max(0, p.block_start[unit]);
     const int re = min(p.M, p.block_start[unit + 1]);
-    for (int c0 = 0; c0 < p.N; c0 += PW) {
-      const Panel<VEC, G, T> pn(p, c0, gl);
+    for (int c0 = c_lo; c0 < c_hi; c0 += PW) {
+      const Panel<VEC, G, T> pn(p, c0, gl, c_hi);
       stream_rows<VEC, G, T, U, LDS>(p, pn, rs, re, gl, gbase, stage);
     }
     return;
@@ -411,8 +397,8 @@ __global__ __launch_bounds__(kWaves * 64) void rowgroup_kernel(Problem p, int pi
   if (row >= p.M) return;
   const int start = p.rowptr[row];
   const int end = p.rowptr[row + 1];
-  for (int c0 = 0; c0 < p.N; c0 += PW) {
-    const Panel<VEC, G, T> pn(p, c0, gl);
+  for (int c0 = c_lo; c0 < c_hi; c0 += PW) {
+    const Panel<VEC, G, T> pn(p, c0, gl, c_hi);
     VT acc[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) acc[t] = Vec<VEC>::zero();
@@ -423,6 +409,39 @@ __global__ __launch_bounds__(kWaves * 64) void rowgroup_kernel(Problem p, int pi
                                        });
     store_row<VEC, T>(p, row, pn.col, pn.cval, acc);
   }
+}
+
+template <int VEC, int G, int T, int U, bool LDS>
+__global__ __launch_bounds__(kWaves * 64) void rowgroup_kernel(Problem p, int piece_blocks,
+                                                                int seg_blocks, int slice_blocks,
+                                                                int slice0) {
+  constexpr int GPW = 64 / G;  // groups per wave
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int gl = lane & (G - 1);
+  const int gbase = lane & ~(G - 1);
+  const int gid = wave * GPW + lane / G;  // group index within block
+
+  __shared__ int2 stage_all[LDS ? kWaves * 64 : 1];
+  int2* stage = stage_all + (LDS ? wave * 64 : 0);
+
+  if constexpr (VEC == 4) {  // column panels are built for float4 columns only
+    if ((int)blockIdx.x < piece_blocks) {
+      pieces_body<VEC, G, T, U, LDS>(p, (int)blockIdx.x, piece_blocks, gl, gbase, gid, stage);
+      return;
+    }
+  }
+  // Column slices: the blocks of slice sl cover columns [c_lo, c_hi), and a
+  // launch holds one slice or all of them in slice order (launch_rg).
+  int bid = (int)blockIdx.x - piece_blocks;
+  int c_lo = 0, c_hi = p.N;
+  if (p.sw > 0) {
+    const int local = bid / slice_blocks;  // bid counts from this launch's first slice, slice0
+    bid -= local * slice_blocks;            // now in [0, slice_blocks)
+    c_lo = (slice0 + local) * p.sw;
+    c_hi = min(p.N, c_lo + p.sw);
+  }
+  rowgroup_block<VEC, G, T, U, LDS>(p, bid, seg_blocks, c_lo, c_hi, gl, gbase, gid, stage);
 }
 
 // One thread per row r in [0, M]: the merge-block starts that fall on r, and
@@ -640,10 +659,17 @@ hipError_t launch_rg(const Problem& p, hipStream_t s) {
     piece_blocks = resident_blocks(reinterpret_cast<const void*>(rowgroup_kernel<VEC, G, T, U, LDS>));
     if (piece_blocks <= 0) return hipErrorInvalidDeviceFunction;
   }
-  const long long blocks = (long long)piece_blocks + unit_blocks + seg_blocks;
-  if (blocks == 0) return hipSuccess;
-  hipLaunchKernelGGL((rowgroup_kernel<VEC, G, T, U, LDS>), dim3((unsigned)blocks), dim3(kWaves * 64),
-                     0, s, p, piece_blocks, seg_blocks);
+  const int slice_blocks = unit_blocks + seg_blocks;
+  const int nslices = p.sw > 0 ? div_up_host(p.N, p.sw) : 1;
+  // Slices in one launch (their blocks in slice order) or one launch per slice.
+  const int per_launch = (p.sw > 0 && p.slice_launch) ? 1 : nslices;
+  for (int s0 = 0; s0 < nslices; s0 += per_launch) {
+    const long long blocks = (long long)piece_blocks + (long long)per_launch * slice_blocks;
+    if (blocks == 0) return hipSuccess;
+    if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((rowgroup_kernel<VEC, G, T, U, LDS>), dim3((unsigned)blocks),
+                       dim3(kWaves * 64), 0, s, p, piece_blocks, seg_blocks, slice_blocks, s0);
+  }
   return hipGetLastError();
 }
 
@@ -655,9 +681,11 @@ static inline int pow2_ceil(int x) {
   return v;
 }
 
+// The kernel shape comes from the columns one block covers: a column slice,
+// or all N.
 template <bool LDS>
 static hipError_t dispatch_vec4(const Problem& p, hipStream_t s) {
-  const int nv = p.N / 4;
+  const int nv = (p.sw > 0 ? std::min(p.sw, p.N) : p.N) / 4;
   const int G = nv >= 64 ? 64 : (pow2_ceil(nv) < 4 ? 4 : pow2_ceil(nv));
   if (G < 64) {
     switch (G) {
@@ -675,7 +703,7 @@ static hipError_t dispatch_vec4(const Problem& p, hipStream_t s) {
 
 template <bool LDS>
 static hipError_t dispatch_vec1(const Problem& p, hipStream_t s) {
-  const int n = p.N;
+  const int n = p.sw > 0 ? std::min(p.sw, p.N) : p.N;
   const int G = n >= 64 ? 64 : (pow2_ceil(n) < 4 ? 4 : pow2_ceil(n));
   if (G < 64) {
     switch (G) {

@@ -1,0 +1,35 @@
+"""Synthetic CSR matrices with chosen row lengths, for the GPU parity tests
+of the long-row paths (column panels, column slices)."""
+import numpy as np
+
+
+def csr_from_lengths(lens, K, seed, narrow=None, unsorted_rows=()):
+    """Rows of the given lengths, columns uniform without replacement in
+    [0, K) (or in narrow[r] = (lo, hi) for chosen rows), sorted unless the
+    row is in unsorted_rows; values U(-1, 1) exact in fp32."""
+    rng = np.random.default_rng(seed)
+    lens = np.asarray(lens, dtype=np.int64)
+    rowptr = np.zeros(lens.size + 1, dtype=np.int32)
+    rowptr[1:] = np.cumsum(lens)
+    cols = []
+    for r, L in enumerate(lens):
+        lo, hi = (narrow or {}).get(r, (0, K))
+        c = rng.choice(hi - lo, size=int(L), replace=False).astype(np.int32) + lo
+        c.sort()
+        if r in unsorted_rows:
+            rng.shuffle(c)
+        cols.append(c)
+    colidx = np.concatenate(cols) if cols else np.zeros(0, np.int32)
+    vals = (rng.integers(0, 1 << 24, size=colidx.size) * 2.0 ** -23 - 1.0).astype(np.float32)
+    return rowptr, colidx.astype(np.int32), vals
+
+
+def mixed_lengths(seed, M=3000):
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(0, 40, size=M)
+    special = [1023, 1024, 1025, 2047, 2048, 2049, 3000, 4096, 5000, 20000, 256, 257, 511, 512, 767,
+               768, 0, 1, 16384]
+    pos = rng.choice(M, size=len(special), replace=False)
+    lens[pos] = special
+    lens[-1] = 6000  # a long row at the very end
+    return lens

@@ -16,43 +16,12 @@ import torch
 
 import oracle
 from csrspmm_amd import ALGORITHMS, capi, gen
+from csr_cases import csr_from_lengths, mixed_lengths
 
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-5
 PANEL_ALGOS = ["WarpPerRowFp4", "WarpPerRowSmemFp4", "Auto"]
-
-
-def csr_from_lengths(lens, K, seed, narrow=None, unsorted_rows=()):
-    """Rows of the given lengths, columns uniform without replacement in
-    [0, K) (or in narrow[r] = (lo, hi) for chosen rows), sorted unless the
-    row is in unsorted_rows; values U(-1, 1) exact in fp32."""
-    rng = np.random.default_rng(seed)
-    lens = np.asarray(lens, dtype=np.int64)
-    rowptr = np.zeros(lens.size + 1, dtype=np.int32)
-    rowptr[1:] = np.cumsum(lens)
-    cols = []
-    for r, L in enumerate(lens):
-        lo, hi = (narrow or {}).get(r, (0, K))
-        c = rng.choice(hi - lo, size=int(L), replace=False).astype(np.int32) + lo
-        c.sort()
-        if r in unsorted_rows:
-            rng.shuffle(c)
-        cols.append(c)
-    colidx = np.concatenate(cols) if cols else np.zeros(0, np.int32)
-    vals = (rng.integers(0, 1 << 24, size=colidx.size) * 2.0 ** -23 - 1.0).astype(np.float32)
-    return rowptr, colidx.astype(np.int32), vals
-
-
-def mixed_lengths(seed, M=3000):
-    rng = np.random.default_rng(seed)
-    lens = rng.integers(0, 40, size=M)
-    special = [1023, 1024, 1025, 2047, 2048, 2049, 3000, 4096, 5000, 20000, 256, 257, 511, 512, 767,
-               768, 0, 1, 16384]
-    pos = rng.choice(M, size=len(special), replace=False)
-    lens[pos] = special
-    lens[-1] = 6000  # a long row at the very end
-    return lens
 
 
 def run(algo, rowptr, colidx, vals, B, dev, C0=None, alpha=1.0, beta=0.0, workspace_bytes=None):
@@ -89,8 +58,10 @@ def panel_bytes(algo, M, K, N, nnz):
 @pytest.mark.parametrize("N", [64, 128, 256])
 @pytest.mark.parametrize("algo", list(ALGORITHMS) + ["Auto"])
 def test_panels_mixed_rows(algo, N, gpu):
-    K = 65536 if N == 64 else 32768  # B = 16 MiB (32 panels) or 16/32 MiB
-    lens = mixed_lengths(7 + N)
+    # B of 16 MiB: panels on, and below the 32 MiB from which column slices
+    # take over at N >= 256
+    K = {64: 65536, 128: 32768, 256: 16384}[N]
+    lens = np.minimum(mixed_lengths(7 + N), K)
     narrow = {int(np.nonzero(lens == 4096)[0][0]): (K // 3, K // 3 + 5000)}  # one panel-ish band
     rowptr, colidx, vals = csr_from_lengths(lens, K, seed=N, narrow=narrow)
     B = gen.dense(11, gen.TAG_B, K, N)
