@@ -449,13 +449,14 @@ __global__ __launch_bounds__(kWaves * 64) void rowgroup_kernel(Problem p, int pi
 // here on each call, from rowptr alone (no counters to reset, no atomics).
 __global__ __launch_bounds__(256) void plan_kernel(Problem p) {
   const int stride = gridDim.x * blockDim.x;
+  const int mshift = __builtin_ctz((unsigned)p.mblk);  // mblk is a power of two
   for (int r = blockIdx.x * blockDim.x + threadIdx.x; r <= p.M; r += stride) {
     const int x0 = clamp_nnz(p.rowptr[r], p.nnz);
     // merge blocks b with F(r-1) < b*mblk <= F(r) start at row r
     const long long F = (long long)r + x0;
     const long long Fprev = r > 0 ? (long long)(r - 1) + clamp_nnz(p.rowptr[r - 1], p.nnz) : -1;
-    const long long b_lo = Fprev < 0 ? 0 : Fprev / p.mblk + 1;
-    const long long b_hi = min(F / p.mblk, (long long)p.nblocks - 1);
+    const long long b_lo = Fprev < 0 ? 0 : (Fprev >> mshift) + 1;
+    const long long b_hi = min(F >> mshift, (long long)p.nblocks - 1);
     for (long long b = b_lo; b <= b_hi; ++b) p.block_start[b] = r;
     if (r == p.M) {
       p.block_start[p.nblocks] = p.M;

@@ -62,6 +62,8 @@ constexpr int kMergeBlock = CSRSPMM_MERGE_BLOCK;
 constexpr int kMergeBlockVec4 = CSRSPMM_MERGE_BLOCK_VEC4;
 constexpr int kMergeBlockMin = kMergeBlock < kMergeBlockVec4 ? kMergeBlock : kMergeBlockVec4;
 constexpr int kMergeBlockMax = kMergeBlock > kMergeBlockVec4 ? kMergeBlock : kMergeBlockVec4;
+static_assert((kMergeBlock & (kMergeBlock - 1)) == 0 && (kMergeBlockVec4 & (kMergeBlockVec4 - 1)) == 0,
+              "merge blocks are powers of two (plan_kernel shifts by them)");
 inline int merge_block(int vec) { return vec == 4 ? kMergeBlockVec4 : kMergeBlock; }
 inline int merge_blocks(int M, int nnz, int mblk) {
   return (int)(((long long)M + nnz + 1 + mblk - 1) / mblk);
