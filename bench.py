@@ -12,6 +12,10 @@ stream.  Prints ONE JSON line:
              event pair around all of the call's launches, recorded by the
              library on the launch stream, csrspmm_timing_*) against 8 TB/s;
              traffic = measured HBM bytes per call from profiles/traffic.json
+  modes      per-call median and mean of the headline variant timed alone:
+             warm (back to back), api (host clock with a device sync, as the
+             reference's spmm() pays) and cold (after a 512 MiB scratch write
+             that flushes L2 and the MALL)
   variants   the same figures for every variant on the same config
   plan       the same figures for a stored plan (csrspmm_plan_*, Auto by
              default) built once outside the timed region, with its build
@@ -48,6 +52,8 @@ def parse():
     ap.add_argument("--variants", default="all", help="'all', 'none' or comma list")
     ap.add_argument("--variant-steps", type=int, default=20)
     ap.add_argument("--plan-algo", default="Auto", help="stored-plan leg ('none' disables it)")
+    ap.add_argument("--mode-calls", type=int, default=30,
+                    help="calls per timing mode (warm / api / cold) of the headline variant")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="time budget of the CPU baseline leg (0 disables it)")
     ap.add_argument("--traffic-file", default=os.path.join(HERE, "profiles", "traffic.json"))
@@ -76,6 +82,49 @@ def time_variant(capi, torch, algo, d, steps, warmup):
     main_ms, calls = capi.timing_read()
     total_ms = start.elapsed_time(stop)
     return total_ms / steps, main_ms / max(calls, 1)
+
+
+def time_modes(capi, torch, algo, d, calls, scratch_mib):
+    """Per-call times of the headline variant in three modes (ms, median and
+    mean over `calls` calls, each timed alone):
+      warm  HIP events around one call, back to back with the previous one;
+      api   host wall clock around one call plus a device synchronize, what
+            the reference's spmm() (src/csrspmm.cpp:73-74) and its bench pay;
+      cold  HIP events around one call after a scratch_mib MiB device write
+            that evicts B, A and C from L2 and the MALL."""
+    stream = torch.cuda.current_stream()
+
+    def call():
+        capi.spmm(algo, d["rowptr"], d["colidx"], d["vals"], d["B"], d["C"], 1.0, 0.0,
+                  workspace=d["ws"])
+
+    scratch = torch.empty(scratch_mib << 18, dtype=torch.float32, device=d["B"].device)
+    out = {}
+    for mode in ("warm", "api", "cold"):
+        call()
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(calls):
+            if mode == "cold":
+                scratch.fill_(1.0)
+            if mode == "api":
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                call()
+                torch.cuda.synchronize()
+                times.append((time.perf_counter() - t0) * 1e3)
+            else:
+                a = torch.cuda.Event(enable_timing=True)
+                b = torch.cuda.Event(enable_timing=True)
+                a.record(stream)
+                call()
+                b.record(stream)
+                b.synchronize()
+                times.append(a.elapsed_time(b))
+        out[mode] = {"median_ms": round(statistics.median(times), 5),
+                     "mean_ms": round(statistics.fmean(times), 5)}
+    del scratch
+    return out
 
 
 def time_plan(capi, torch, algo, d, K, N, steps, warmup):
@@ -197,6 +246,11 @@ def main():
             variants[name] = figures(vms, vmain)
             print(f"[bench] {name}: {vms:.4f} ms/call", file=sys.stderr, flush=True)
 
+    modes = None
+    if args.mode_calls > 0:
+        modes = time_modes(capi, torch, args.algo, d, args.mode_calls, 512)
+        print(f"[bench] modes: {modes}", file=sys.stderr, flush=True)
+
     plan_fig = None
     if args.plan_algo != "none":
         plan, build_ms, pms, pmain = time_plan(capi, torch, args.plan_algo, d, a.K, N,
@@ -244,6 +298,7 @@ def main():
                      "traffic": traffic, "kernel": f"{resolved}: all launches of one call",
                      "kernel_ms": round(main_ms, 5)},
         "cpu_baseline": cpu,
+        "modes": modes,
         "variants": variants,
         "plan": plan_fig,
     }

@@ -241,6 +241,11 @@ int spmm_impl(int algo_in, int M, int K, int N, int nnz, const int* rowptr, cons
     WorkspaceLayout L = workspace_layout(M, K, N, nnz, P);
     if (owned) {
       st = owned_workspace(stream, L.total, &ws);
+      if (st == CSRSPMM_STATUS_ALLOC_FAILED && L.total > L.base_total) {
+        // no room for the panel tables: run without them
+        L = workspace_layout(M, K, N, nnz, 0);
+        st = owned_workspace(stream, L.total, &ws);
+      }
       if (st != 0) return st;
     } else {
       if (!ws || ws_bytes < L.base_total) return CSRSPMM_STATUS_WORKSPACE_TOO_SMALL;
