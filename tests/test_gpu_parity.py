@@ -111,7 +111,7 @@ def sample_rows(a, full):
 
 
 @pytest.mark.parametrize("algo", ALGORITHMS)
-@pytest.mark.parametrize("cfg_name", ["host", "medium", "large", "xl", "rmat", "rmat512"])
+@pytest.mark.parametrize("cfg_name", ["host", "medium", "large", "xl", "rmat", "rmat512", "xl98"])
 def test_config(cfg_name, algo, gpu):
     cfg, a, B = config_data(cfg_name)
     print(f"[parity] {cfg_name} {algo} M={a.M} nnz={a.nnz} N={cfg.N}", flush=True)
