@@ -17,11 +17,11 @@
 //     holds the position where the panel index first reaches q.
 //  2. panel_sched_kernel, one workgroup: compacts the flagged rows into
 //     list[] in row order (at most nl_max of them; pidx[id] = their index,
-//     -1 elsewhere), estimates the load of each panel from up to
-//     kDevPanelSample evenly spaced rows, turns panels off for this call when
-//     the heaviest panel carries more than kPanelSkewMax times the mean (hot
-//     columns, as in R-MAT, already give L2 reuse), and cuts the panels into
-//     kXcds contiguous ranges of near-equal load.
+//     -1 elsewhere), gives XCD x the panels [x P / 8, (x + 1) P / 8), and
+//     estimates the panel loads from up to kDevPanelSample evenly spaced rows
+//     to turn panels off for this call when the heaviest panel carries more
+//     than kPanelSkewMax times the mean (hot columns, as in R-MAT, already
+//     give L2 reuse) or the heaviest XCD range more than 1.5 times the mean.
 //
 // The pieces kernel (rowgroup.hip) then lets the workgroups of XCD x walk
 // the pieces (panel, row) of range x in panel order; the main kernel and the
@@ -37,6 +37,7 @@ namespace csrspmm_hip {
 namespace {
 
 constexpr int kSchedThreads = 1024;
+constexpr int kXcdSkewMax2 = 3;  // heaviest XCD range at most 1.5 (= 3 / 2) x the mean
 
 __device__ __forceinline__ int clampi(int x, int lo, int hi) { return min(max(x, lo), hi); }
 
@@ -185,48 +186,43 @@ __global__ __launch_bounds__(kSchedThreads) void panel_sched_kernel(Problem p) {
   }
   __syncthreads();
 
-  // 3. Skew rule and the XCD ranges (wave 0; lane l holds panels 4l .. 4l+3):
-  // range x ends after the leading panels whose load prefix stays within
-  // x / kXcds of the total.
+  // 3. XCD ranges and the skew rules (wave 0; lane l holds panels 4l .. 4l+3).
+  // XCD x takes the panels [x P / kXcds, (x + 1) P / kXcds): equal ranges, so
+  // the host can size the pieces grid.  Panels stay off for this call when
+  // the heaviest panel carries more than kPanelSkewMax times the mean panel
+  // load, or the heaviest XCD range more than kXcdSkewMax times the mean.
   if (wave != 0) return;
-  long long wq[4], pre[4];
-  long long local = 0, mx = 0;
+  long long wq[4];
+  long long total = 0, mx = 0;
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int q = 4 * lane + u;
     wq[u] = q < P ? s_w[q] : 0;
-    local += wq[u];
+    total += wq[u];
     mx = max(mx, wq[u]);
   }
-  const long long incl = wave_incl_scan(local, lane);
-  const long long total = __shfl(incl, 63);
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) mx = max(mx, __shfl_xor(mx, off));
-  long long run = incl - local;
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    run += wq[u];
-    pre[u] = run;
+  for (int off = 32; off > 0; off >>= 1) {
+    total += __shfl_xor(total, off);
+    mx = max(mx, __shfl_xor(mx, off));
   }
-  const bool skewed = total > 0 && mx * P > (long long)kPanelSkewMax * total;
-  for (int x = 1; x < kXcds; ++x) {
-    int c = 0;
-    if (total > 0) {
-      const long long target = total * x / kXcds;
+  long long xmax = 0;
+  for (int x = 0; x < kXcds; ++x) {
+    const int q0 = (int)((long long)P * x / kXcds), q1 = (int)((long long)P * (x + 1) / kXcds);
+    long long lx = 0;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) c += (4 * lane + u < P && pre[u] <= target) ? 1 : 0;
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) c += __shfl_xor(c, off);
-    } else {
-      c = (int)((long long)P * x / kXcds);
+    for (int u = 0; u < 4; ++u) {
+      const int q = 4 * lane + u;
+      if (q >= q0 && q < q1) lx += wq[u];
     }
-    if (lane == 0) d.sched[1 + x] = c;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) lx += __shfl_xor(lx, off);
+    xmax = max(xmax, lx);
   }
-  if (lane == 0) {
-    d.sched[0] = skewed ? 0 : nl;
-    d.sched[1] = 0;
-    d.sched[1 + kXcds] = P;
-  }
+  const bool skewed = total > 0 && (mx * P > (long long)kPanelSkewMax * total ||
+                                    xmax * kXcds * 2 > (long long)kXcdSkewMax2 * total);
+  if (lane <= kXcds) d.sched[1 + lane] = (int)((long long)P * lane / kXcds);
+  if (lane == 0) d.sched[0] = skewed ? 0 : nl;
 }
 
 }  // namespace

@@ -30,9 +30,6 @@
 
 #include "common.hpp"
 
-#include <map>
-#include <mutex>
-#include <utility>
 
 namespace csrspmm_hip {
 
@@ -59,6 +56,13 @@ constexpr int kVec4U = CSRSPMM_VEC4_UNROLL;
 #define CSRSPMM_SEG_UNROLL 4
 #endif
 
+
+// Pieces per group in one pieces block (a chunk is kPiecesPerGroup * GPB
+// consecutive pieces of an XCD's list); build-time tunable.
+#ifndef CSRSPMM_PIECES_PER_GROUP
+#define CSRSPMM_PIECES_PER_GROUP 2
+#endif
+constexpr int kPiecesPerGroup = CSRSPMM_PIECES_PER_GROUP;
 
 // B-row gathers in flight per lane in the pieces kernel; build-time tunable.
 #ifndef CSRSPMM_PIECE_UNROLL
@@ -245,19 +249,21 @@ __device__ __forceinline__ void stream_rows(const Problem& p, const Panel<VEC, G
 }
 
 // Pieces of this call's column panels, run by the first blocks of the main
-// launch.  Pieces block b runs on XCD b mod kXcds and shares with the other
-// pieces blocks of that XCD the pieces of its panel range [qa, qb): piece i
-// is (panel qa + i / nl, panelized row i mod nl), the nonzeros of that row
-// whose columns fall in the panel, summed into the partial (row, panel).
-// Pieces are dealt group-strided in panel order, so the groups of an XCD
-// work within a few panels at a time and gather from a band of B that stays
-// in that XCD's L2.  The pieces blocks are as many as the GPU holds at once
-// and come first in the grid; the short-row and segment blocks behind them
-// take over each slot as its pieces run out, which absorbs the uneven finish
-// of static dealing.
+// launch.  Pieces block b takes chunk b / kXcds of XCD b mod kXcds's piece
+// list: kPiecesPerGroup * GPB consecutive pieces, group g taking pieces
+// g, g + GPB, ... of the chunk.  XCD x's list holds, panel by panel through
+// its range [qa, qb), piece i = (panel qa + i / nl, panelized row i mod nl):
+// the nonzeros of that row whose columns fall in the panel, summed into the
+// partial (row, panel).  Block b runs on XCD b mod kXcds, and blocks are
+// dispatched in order, so the running blocks of an XCD hold a short stretch
+// of its list, within a panel or two, and gather from a band of B that stays
+// in that XCD's L2; the hardware dispatcher balances the uneven pieces.  The
+// grid covers nl_max rows (the host cannot know nl); chunks past the list
+// exit at once, and they come last.  The short-row and segment blocks follow
+// in the same grid and take over slots as the pieces run out.
 template <int VEC, int G, int T, int U, bool LDS>
-__device__ __forceinline__ void pieces_body(const Problem& p, int block, int nblocks, int gl,
-                                            int gbase, int gid, int2* stage) {
+__device__ __forceinline__ void pieces_body(const Problem& p, int block, int gl, int gbase, int gid,
+                                            int2* stage) {
   using VT = typename Vec<VEC>::T;
   constexpr int GPB = kWaves * (64 / G);
   constexpr int PW = G * VEC * T;
@@ -267,9 +273,12 @@ __device__ __forceinline__ void pieces_body(const Problem& p, int block, int nbl
   if (nl <= 0) return;
   const int x = block % kXcds;
   const int qa = d.sched[1 + x];
-  const unsigned n = (unsigned)max(d.sched[2 + x] - qa, 0) * (unsigned)nl;
-  const unsigned stride = (unsigned)((nblocks / kXcds) * GPB);
-  unsigned i = (unsigned)((block / kXcds) * GPB + gid);
+  const unsigned n_all = (unsigned)max(d.sched[2 + x] - qa, 0) * (unsigned)nl;
+  const unsigned first = (unsigned)(block / kXcds) * (unsigned)(kPiecesPerGroup * GPB);
+  if (first >= n_all) return;
+  const unsigned n = min(n_all, first + (unsigned)(kPiecesPerGroup * GPB));
+  const unsigned stride = (unsigned)GPB;
+  unsigned i = first + (unsigned)gid;
   if (i >= n) return;
   const int P1 = d.P + 1;
   auto bounds = [&](unsigned k, int id, int& a, int& e) {
@@ -427,7 +436,7 @@ __global__ __launch_bounds__(kWaves * 64) void rowgroup_kernel(Problem p, int pi
 
   if constexpr (VEC == 4) {  // column panels are built for float4 columns only
     if ((int)blockIdx.x < piece_blocks) {
-      pieces_body<VEC, G, T, U, LDS>(p, (int)blockIdx.x, piece_blocks, gl, gbase, gid, stage);
+      pieces_body<VEC, G, T, U, LDS>(p, (int)blockIdx.x, gl, gbase, gid, stage);
       return;
     }
   }
@@ -627,27 +636,6 @@ void launch_combine(const Problem& p, hipStream_t s) {
   }
 }
 
-// Blocks of 256 threads of `kernel` the current device holds at once (CUs x
-// blocks per CU), a multiple of kXcds; cached per kernel and device.
-int resident_blocks(const void* kernel) {
-  static std::mutex mu;
-  static std::map<std::pair<const void*, int>, int> cache;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 0;
-  std::lock_guard<std::mutex> lock(mu);
-  auto it = cache.find({kernel, dev});
-  if (it != cache.end()) return it->second;
-  int per_cu = 0, cus = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kWaves * 64, 0) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
-    (void)hipGetLastError();
-    return 0;
-  }
-  const int n = std::max(kXcds, (per_cu * cus) / kXcds * kXcds);
-  cache[{kernel, dev}] = n;
-  return n;
-}
-
 template <int VEC, int G, int T, int U, bool LDS>
 hipError_t launch_rg(const Problem& p, hipStream_t s) {
   constexpr int GPB = kWaves * (64 / G);
@@ -657,8 +645,11 @@ hipError_t launch_rg(const Problem& p, hipStream_t s) {
       (p.plan && p.nslots > 0) ? std::min(kSegBlocksMax, div_up_host(p.nslots, GPB)) : 0;
   int piece_blocks = 0;
   if (VEC == 4 && p.dp.P > 0) {
-    piece_blocks = resident_blocks(reinterpret_cast<const void*>(rowgroup_kernel<VEC, G, T, U, LDS>));
-    if (piece_blocks <= 0) return hipErrorInvalidDeviceFunction;
+    // chunks of the longest XCD list possible: ceil(P / kXcds) panels x nl_max rows
+    const long long per_xcd = (long long)div_up_host(p.dp.P, kXcds) * p.dp.nl_max;
+    const long long chunks = (per_xcd + (long long)kPiecesPerGroup * GPB - 1) / ((long long)kPiecesPerGroup * GPB);
+    if (chunks * kXcds > 0x7fffffffLL / 2) return hipErrorInvalidValue;
+    piece_blocks = (int)(chunks * kXcds);
   }
   const int slice_blocks = unit_blocks + seg_blocks;
   const int nslices = p.sw > 0 ? div_up_host(p.N, p.sw) : 1;
