@@ -136,3 +136,20 @@ def test_panels_base_workspace_runs_without_panels(algo, gpu):
     whole = np.diff(rowptr) <= 511
     assert np.array_equal(C_base[whole].view(np.uint32), C_full[whole].view(np.uint32))
 
+
+
+@pytest.mark.parametrize("algo", PANEL_ALGOS)
+@pytest.mark.parametrize("K", [50000, 98765])
+def test_panels_odd_k(algo, K, gpu):
+    # K not a power of two: the panel width is ceil(K / P) rounded up to a
+    # power of two, so fewer panels than panel_count cover the columns and
+    # the last one is partial
+    N = 128 if K == 50000 else 64  # B of 24 / 24 MiB
+    lens = np.minimum(mixed_lengths(K % 97), K)
+    rowptr, colidx, vals = csr_from_lengths(lens, K, seed=K)
+    B = gen.dense(16, gen.TAG_B, K, N)
+    base, full = panel_bytes(algo, lens.size, K, N, colidx.size)
+    if algo != "Auto" or N >= 128:
+        assert full > base
+    C = run(algo, rowptr, colidx, vals, B, gpu)
+    check(algo, C, rowptr, colidx, vals, B, what=f"K={K}")
