@@ -10,7 +10,9 @@ FETCH_SIZE / WRITE_SIZE readings calibrate the counters.
         --config xl --algo Auto --plan --calls 20
 
 With --plan the calls go through one stored plan (csrspmm_plan_*) built
-before the first call.
+before the first call.  With --no-panels each call gets a workspace of
+csrspmm_workspace_bytes (the base size), which runs without per-call column
+panels: the counters of the two runs show what the panels change.
 """
 from __future__ import annotations
 
@@ -25,6 +27,8 @@ def main(argv=None):
     ap.add_argument("--algo", default="WarpPerRowFp4")
     ap.add_argument("--calls", type=int, default=20)
     ap.add_argument("--plan", action="store_true", help="call through a stored plan")
+    ap.add_argument("--no-panels", action="store_true",
+                    help="pass a base-size workspace, so the call runs without column panels")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run one device-to-device copy of this many MiB")
     args = ap.parse_args(argv)
@@ -57,12 +61,18 @@ def main(argv=None):
         torch.cuda.synchronize()
         print(f"[profile_run] plan {plan.algorithm}: {plan.panelized_rows} panelized rows, "
               f"{plan.device_bytes} device bytes", flush=True)
+    ws = None
+    if args.no_panels:
+        algo = capi.ALGO[args.algo]
+        ws = torch.empty(max(capi.hip().csrspmm_workspace_bytes(algo, a.M, cfg.N, a.nnz), 1),
+                         dtype=torch.uint8, device=dev)
+        print(f"[profile_run] base workspace of {ws.numel()} bytes: no column panels", flush=True)
     t0 = time.perf_counter()
     for i in range(args.calls):
         if plan is not None:
             plan.spmm(dB, C, 1.0, 0.0)
         else:
-            capi.spmm(args.algo, rp, ci, va, dB, C, 1.0, 0.0)
+            capi.spmm(args.algo, rp, ci, va, dB, C, 1.0, 0.0, workspace=ws)
     torch.cuda.synchronize()
     print(f"[profile_run] {args.calls} calls in {time.perf_counter() - t0:.3f}s", flush=True)
     if plan is not None:
