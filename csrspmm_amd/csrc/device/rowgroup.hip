@@ -39,7 +39,7 @@ constexpr int kWaves = 4;  // waves per block (256 threads)
 
 // Blocks of the combine kernel that scan the segment slots (grid-strided).
 #ifndef CSRSPMM_COMBINE_SCAN_BLOCKS
-#define CSRSPMM_COMBINE_SCAN_BLOCKS 1024
+#define CSRSPMM_COMBINE_SCAN_BLOCKS 4096
 #endif
 constexpr int kCombineScanBlocks = CSRSPMM_COMBINE_SCAN_BLOCKS;
 
@@ -453,59 +453,94 @@ __global__ __launch_bounds__(kWaves * 64) void rowgroup_kernel(Problem p, int pi
   rowgroup_block<VEC, G, T, U, LDS>(p, bid, seg_blocks, c_lo, c_hi, gl, gbase, gid, stage);
 }
 
-// One thread per row r in [0, M]: the merge-block starts that fall on r, and
-// the segment slots r owns.  Every entry the main kernel reads is written
-// here on each call, from rowptr alone (no counters to reset, no atomics).
+// Table entries of one row r: the merge-block starts [b_lo, b_hi], the
+// segment slots [s0, s1) (the first nseg hold segments) and the windows
+// [w0, w1), each range walked from `first` in steps of `step`.
+__device__ __forceinline__ void plan_row_entries(const Problem& p, int r, int b_lo, int b_hi, int s0,
+                                                 int s1, int nseg, int w0, int w1, int x0, int x1,
+                                                 int first, int step) {
+  for (int b = b_lo + first; b <= b_hi; b += step) p.block_start[b] = r;
+  for (int s = s0 + first; s < s1; s += step)
+    p.seg_info[s] = (s - s0) < nseg ? make_int2(r, s - s0) : make_int2(-1, 0);
+  // the first window of a long row is the row's id
+  for (int w = w0 + first; w < w1; w += step)
+    p.dp.win[w] = make_int4(r, x0, x1, (w == w0 && x1 - x0 >= kPanelMinLen) ? 1 : 0);
+}
+
+// A row with more table entries than this has them written by its whole
+// wave, 64 per store instruction, instead of by its own lane one at a time
+// (a long row covers hundreds of merge blocks, and one lane can hold only a
+// few dozen stores in flight).
+constexpr int kPlanSoloEntries = 8;
+
+// One thread per row r in [0, M]: the merge-block starts that fall on r, the
+// segment slots r owns and, with column panels, the windows that begin in r.
+// Every entry the main kernel reads is written here on each call, from
+// rowptr alone (no counters to reset, no atomics).
 __global__ __launch_bounds__(256) void plan_kernel(Problem p) {
   const int stride = gridDim.x * blockDim.x;
   const int mshift = __builtin_ctz((unsigned)p.mblk);  // mblk is a power of two
-  for (int r = blockIdx.x * blockDim.x + threadIdx.x; r <= p.M; r += stride) {
-    const int x0 = clamp_nnz(p.rowptr[r], p.nnz);
-    // merge blocks b with F(r-1) < b*mblk <= F(r) start at row r
-    const long long F = (long long)r + x0;
-    const long long Fprev = r > 0 ? (long long)(r - 1) + clamp_nnz(p.rowptr[r - 1], p.nnz) : -1;
-    const long long b_lo = Fprev < 0 ? 0 : (Fprev >> mshift) + 1;
-    const long long b_hi = min(F >> mshift, (long long)p.nblocks - 1);
-    for (long long b = b_lo; b <= b_hi; ++b) p.block_start[b] = r;
-    if (r == p.M) {
-      p.block_start[p.nblocks] = p.M;
-      continue;
+  const int lane = lane_id();
+  // block-uniform trip count, so every wave reaches the ballot below whole
+  for (int base = blockIdx.x * blockDim.x; base <= p.M; base += stride) {
+    const int r = base + (int)threadIdx.x;
+    int b_lo = 0, b_hi = -1, s0 = 0, s1 = 0, nseg = 0, w0 = 0, w1 = 0, x0 = 0, x1 = 0;
+    if (r <= p.M) {
+      x0 = clamp_nnz(p.rowptr[r], p.nnz);
+      // merge blocks b with F(r-1) < b*mblk <= F(r) start at row r
+      const long long F = (long long)r + x0;
+      const long long Fprev = r > 0 ? (long long)(r - 1) + clamp_nnz(p.rowptr[r - 1], p.nnz) : -1;
+      b_lo = Fprev < 0 ? 0 : (int)((Fprev >> mshift) + 1);
+      b_hi = (int)min(F >> mshift, (long long)p.nblocks - 1);
+      if (r == p.M) {
+        p.block_start[p.nblocks] = p.M;
+      } else {
+        // slots [x0 / S, x1 / S) belong to row r; a long row uses the first nseg
+        x1 = clamp_nnz(p.rowptr[r + 1], p.nnz);
+        s0 = x0 / kSegLen;
+        s1 = min(max(s0, x1 / kSegLen), p.nslots);
+        const int len = x1 - x0;
+        nseg = len > kLongRow ? len / kSegLen : 0;
+        if (p.dp.P > 0) {
+          // windows w whose first position w * kPanelMinLen lies in this row
+          w0 = (x0 + kPanelMinLen - 1) / kPanelMinLen;
+          w1 = max(w0, min((x1 + kPanelMinLen - 1) / kPanelMinLen, p.dp.nwin));
+        }
+      }
     }
-    // slots [x0 / S, x1 / S) belong to row r; a long row uses the first nseg
-    const int x1 = clamp_nnz(p.rowptr[r + 1], p.nnz);
-    const int s0 = x0 / kSegLen;
-    const int s1 = min(max(s0, x1 / kSegLen), p.nslots);
-    const int len = x1 - x0;
-    const int nseg = len > kLongRow ? len / kSegLen : 0;
-    for (int s = s0; s < s1; ++s)
-      p.seg_info[s] = (s - s0) < nseg ? make_int2(r, s - s0) : make_int2(-1, 0);
-    if (p.dp.P > 0) {
-      // windows w whose first position w * kPanelMinLen lies in this row; the
-      // first of them is the row's id when the row is long
-      const int w0 = (x0 + kPanelMinLen - 1) / kPanelMinLen;
-      const int w1 = min((x1 + kPanelMinLen - 1) / kPanelMinLen, p.dp.nwin);
-      for (int w = w0; w < w1; ++w)
-        p.dp.win[w] = make_int4(r, x0, x1, (w == w0 && len >= kPanelMinLen) ? 1 : 0);
+    const int entries = max(b_hi - b_lo + 1, 0) + (s1 - s0) + (w1 - w0);
+    const bool solo = entries <= kPlanSoloEntries;
+    if (solo) plan_row_entries(p, r, b_lo, b_hi, s0, s1, nseg, w0, w1, x0, x1, 0, 1);
+    unsigned long long heavy = __ballot(!solo);
+    while (heavy) {
+      const int l = __ffsll((long long)heavy) - 1;
+      heavy &= heavy - 1;
+      plan_row_entries(p, __builtin_amdgcn_readlane(r, l), __builtin_amdgcn_readlane(b_lo, l),
+                       __builtin_amdgcn_readlane(b_hi, l), __builtin_amdgcn_readlane(s0, l),
+                       __builtin_amdgcn_readlane(s1, l), __builtin_amdgcn_readlane(nseg, l),
+                       __builtin_amdgcn_readlane(w0, l), __builtin_amdgcn_readlane(w1, l),
+                       __builtin_amdgcn_readlane(x0, l), __builtin_amdgcn_readlane(x1, l), lane, 64);
     }
   }
 }
 
-// Partials k = q, q + NG, q + 2*NG, ... (k < n) of one lane's columns, added
-// in that order; partial k sits at src + idx(k) * ldp, idx(k) = pieces[k]
-// when a piece list is given, else k.
-template <int VEC, int NG>
-__device__ __forceinline__ typename Vec<VEC>::T sum_strided(const float* src, const int* pieces,
-                                                            int n, int q, long long ldp, bool cv) {
-  using VT = typename Vec<VEC>::T;
-  VT acc = Vec<VEC>::zero();
+// Partials k = q, q + NG, q + 2*NG, ... (k < n) of one lane's four columns,
+// added in that order; partial k sits at src + idx(k) * ldp, idx(k) =
+// pieces[k] when a piece list is given, else k.  Partial rows are ldp = N
+// rounded up to 4 floats long and 256-byte aligned, so they are read as
+// float4 whatever the alignment of C.
+template <int NG>
+__device__ __forceinline__ f4 sum_strided(const float* src, const int* pieces, int n, int q,
+                                          long long ldp, bool cv) {
+  f4 acc = Vec<4>::zero();
   if (!cv) return acc;
-  auto part = [&](int k) -> VT {
+  auto part = [&](int k) -> f4 {
     const long long idx = pieces ? (long long)pieces[k] : (long long)k;
-    return *reinterpret_cast<const VT*>(src + idx * ldp);
+    return *reinterpret_cast<const f4*>(src + idx * ldp);
   };
   int k = q;
   for (; k + 7 * NG < n; k += 8 * NG) {
-    VT a[8];
+    f4 a[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) a[u] = part(k + u * NG);
 #pragma unroll
@@ -518,12 +553,6 @@ __device__ __forceinline__ typename Vec<VEC>::T sum_strided(const float* src, co
 // Sum over the 64 / GC lane groups of a wave by a fixed xor-shuffle tree;
 // every group ends with the total.
 template <int GC>
-__device__ __forceinline__ float wave_group_sum(float v) {
-#pragma unroll
-  for (int off = GC; off < 64; off <<= 1) v += __shfl_xor(v, off);
-  return v;
-}
-template <int GC>
 __device__ __forceinline__ f4 wave_group_sum(f4 v) {
 #pragma unroll
   for (int off = GC; off < 64; off <<= 1) {
@@ -535,54 +564,77 @@ __device__ __forceinline__ f4 wave_group_sum(f4 v) {
   return v;
 }
 
+// Columns c .. c + 3 of a C row (those below N): one float4 store when C
+// rows are 16-byte aligned (VEC == 4, N % 4 == 0), else one per column.
+template <int VEC>
+__device__ __forceinline__ void store_cols4(const Problem& p, float* cptr, int c, f4 v) {
+  if constexpr (VEC == 4) {
+    store_epi<4>(p, cptr, v);
+  } else {
+    store_epi<1>(p, cptr, v.x);
+    if (c + 1 < p.N) store_epi<1>(p, cptr + 1, v.y);
+    if (c + 2 < p.N) store_epi<1>(p, cptr + 2, v.z);
+    if (c + 3 < p.N) store_epi<1>(p, cptr + 3, v.w);
+  }
+}
+
+// Segment slots one wave of the combine scan reads at once.  A split row
+// spans two slots or more, so a wave meets at most kScanSlots / 2 rows.
+constexpr int kScanSlots = 16;
+
 // C rows of split long rows (one partial per segment) and of panelized rows
 // (one partial per piece), each the sum of its partials in a fixed order, so
 // results repeat bit for bit.  A wave's lanes form P = 64 / GC groups of GC
-// lanes, each group covering GC * VEC columns.
-//  * Blocks [0, scan_blocks): a wave reads 64 consecutive segment slots at
-//    once, finds by ballot the rows whose first segment lies among them, and
-//    sums the segments of each such row that has two or more: group q takes segments q, q + P, ..., then
-//    the P group sums meet in the xor tree.
+// lanes, each group covering 4 * GC columns (float4 per lane).
+//  * Blocks [0, scan_blocks): a wave reads kScanSlots consecutive segment
+//    slots, loads the length of every row whose first segment lies among
+//    them (all at once), and sums the segments of each such row that has two
+//    or more: group q takes segments q, q + P, ..., then the P group sums
+//    meet in the xor tree.
 //  * Blocks [scan_blocks, ...): one panelized row per block.  Its 4 waves'
 //    4P groups split the pieces the same way; each wave's sum goes to LDS and
 //    wave 0 adds the four in wave order.
 template <int VEC, int GC>
 __global__ __launch_bounds__(kWaves * 64) void combine_kernel(Problem p, int scan_blocks) {
-  using VT = typename Vec<VEC>::T;
   constexpr int P = 64 / GC;
   const int lane = lane_id();
   const int q = lane / GC;
   const int gl = lane & (GC - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if ((int)blockIdx.x < scan_blocks) {
-    const int nchunks = div_up(p.nslots, 64);
+    const int nchunks = div_up(p.nslots, kScanSlots);
     for (int ch = blockIdx.x * kWaves + wave; ch < nchunks; ch += scan_blocks * kWaves) {
-      const int s = ch * 64 + lane;
+      const int s = ch * kScanSlots + lane;
       int2 si = make_int2(-1, 1);
-      if (s < p.nslots) si = p.seg_info[s];
-      unsigned long long firsts = __ballot(si.x >= 0 && si.x < p.M && si.y == 0);
-      while (firsts) {
-        const int l = __ffsll((long long)firsts) - 1;
-        firsts &= firsts - 1;
+      if (lane < kScanSlots && s < p.nslots) si = p.seg_info[s];
+      int nseg = 0;
+      if (si.x >= 0 && si.x < p.M && si.y == 0) {
+        const int x0 = p.rowptr[si.x];
+        const int len = p.rowptr[si.x + 1] - x0;
+        nseg = len / kSegLen;
+        // one segment: stored by the segment phase; panelized: summed from pieces
+        if (nseg < 2 || (len >= kPanelMinLen && is_panelized(p, x0))) nseg = 0;
+      }
+      unsigned long long rows = __ballot(nseg > 0);
+      while (rows) {
+        const int l = __ffsll((long long)rows) - 1;
+        rows &= rows - 1;
         const int row = __builtin_amdgcn_readlane(si.x, l);
-        const int len = p.rowptr[row + 1] - p.rowptr[row];
-        const int nseg = len / kSegLen;
-        if (nseg < 2) continue;  // stored by the segment phase
-        if (len >= kPanelMinLen && is_panelized(p, p.rowptr[row])) continue;  // summed from pieces
-        const float* base = p.partials + (long long)(ch * 64 + l) * p.ldp;
+        const int n = __builtin_amdgcn_readlane(nseg, l);
+        const float* base = p.partials + (long long)(ch * kScanSlots + l) * p.ldp;
         float* crow = p.C + (long long)row * p.ldc;
-        for (int c0 = 0; c0 < p.N; c0 += GC * VEC) {
-          const int c = c0 + gl * VEC;
+        for (int c0 = 0; c0 < p.N; c0 += GC * 4) {
+          const int c = c0 + gl * 4;
           const bool cv = c < p.N;
-          const VT acc = wave_group_sum<GC>(sum_strided<VEC, P>(base + c, nullptr, nseg, q, p.ldp, cv));
-          if (q == 0 && cv) store_epi<VEC>(p, crow + c, acc);
+          const f4 acc = wave_group_sum<GC>(sum_strided<P>(base + c, nullptr, n, q, p.ldp, cv));
+          if (q == 0 && cv) store_cols4<VEC>(p, crow + c, c, acc);
         }
       }
     }
     return;
   }
   const int i = (int)blockIdx.x - scan_blocks;
-  __shared__ VT wave_sum[kWaves][GC];
+  __shared__ f4 wave_sum[kWaves][GC];
   int row, npc;
   const int* pieces;
   const float* part;
@@ -602,27 +654,29 @@ __global__ __launch_bounds__(kWaves * 64) void combine_kernel(Problem p, int sca
     part = p.pan_part;
   }
   float* crow = p.C + (long long)row * p.ldc;
-  for (int c0 = 0; c0 < p.N; c0 += GC * VEC) {
-    const int c = c0 + gl * VEC;
+  for (int c0 = 0; c0 < p.N; c0 += GC * 4) {
+    const int c = c0 + gl * 4;
     const bool cv = c < p.N;
-    const VT acc = wave_group_sum<GC>(
-        sum_strided<VEC, kWaves * P>(part + c, pieces, npc, wave * P + q, p.ldp, cv));
+    const f4 acc = wave_group_sum<GC>(
+        sum_strided<kWaves * P>(part + c, pieces, npc, wave * P + q, p.ldp, cv));
     if (q == 0) wave_sum[wave][gl] = acc;
     __syncthreads();
     if (wave == 0 && q == 0 && cv) {
-      VT t = wave_sum[0][gl];
+      f4 t = wave_sum[0][gl];
 #pragma unroll
       for (int w = 1; w < kWaves; ++w) t = add_v(t, wave_sum[w][gl]);
-      store_epi<VEC>(p, crow + c, t);
+      store_cols4<VEC>(p, crow + c, c, t);
     }
     __syncthreads();
   }
 }
 
+// The lane groups cover ceil(N / 4) float4 column chunks.
 template <int VEC>
 void launch_combine(const Problem& p, hipStream_t s) {
-  const int chunks = (p.N + VEC - 1) / VEC;
-  const int scan_blocks = std::min(kCombineScanBlocks, div_up_host(div_up_host(p.nslots, 64), kWaves));
+  const int chunks = (p.N + 3) / 4;
+  const int scan_blocks =
+      std::min(kCombineScanBlocks, div_up_host(div_up_host(p.nslots, kScanSlots), kWaves));
   const int blocks = scan_blocks + (p.dp.P > 0 ? p.dp.nl_max : p.npan);
   if (blocks == 0) return;
   if (chunks <= 8) {
@@ -655,12 +709,18 @@ hipError_t launch_rg(const Problem& p, hipStream_t s) {
   const int nslices = p.sw > 0 ? div_up_host(p.N, p.sw) : 1;
   // Slices in one launch (their blocks in slice order) or one launch per slice.
   const int per_launch = (p.sw > 0 && p.slice_launch) ? 1 : nslices;
+  // Unused LDS that leaves room for only `cap` blocks per CU (a multiple of
+  // 512 bytes, the allocation unit, per block with the static stage).
+  const int cap = slice_blocks_per_cu(p.K, p.sw, p.slice_launch);
+  constexpr int kStaticLds = (LDS ? kWaves * 64 : 1) * (int)sizeof(int2);
+  const int pad_lds = cap > 0 ? (kLdsPerCu / cap) / 512 * 512 - kStaticLds : 0;
   for (int s0 = 0; s0 < nslices; s0 += per_launch) {
     const long long blocks = (long long)piece_blocks + (long long)per_launch * slice_blocks;
     if (blocks == 0) return hipSuccess;
     if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
     hipLaunchKernelGGL((rowgroup_kernel<VEC, G, T, U, LDS>), dim3((unsigned)blocks),
-                       dim3(kWaves * 64), 0, s, p, piece_blocks, seg_blocks, slice_blocks, s0);
+                       dim3(kWaves * 64), pad_lds, s, p, piece_blocks, seg_blocks, slice_blocks,
+                       s0);
   }
   return hipGetLastError();
 }

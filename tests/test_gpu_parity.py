@@ -188,6 +188,37 @@ def test_strided_b_and_split_boundaries(algo, gpu):
 
 
 @pytest.mark.parametrize("algo", ALGORITHMS)
+@pytest.mark.parametrize("N", [1, 3, 5, 130])
+def test_split_rows_odd_columns(algo, N, gpu):
+    """Split rows at column counts that are not a multiple of 4, with C rows
+    that are not 16-byte aligned: the combine reads partials four columns at
+    a time and stores C column by column.  Runs of consecutive long rows put
+    several split rows in one scan chunk of the combine, and many rows with
+    long table ranges (merge-block starts, segment slots) in one wave of the
+    per-call plan."""
+    K = 20000
+    lens = np.concatenate([[20000, 0, 3], np.full(40, 520), [700, 1, 0], np.full(70, 600),
+                           np.arange(64) % 5, [1500, 9000]]).astype(np.int64)
+    rng = np.random.default_rng(100 + N)
+    rowptr = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    colidx = np.concatenate([np.sort(rng.choice(K, L, replace=False)) for L in lens]).astype(np.int32)
+    vals = rng.uniform(-1, 1, colidx.size).astype(np.float32)
+    B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+    M = lens.size
+    dev = gpu
+    drp, dci, dv, dB = dev_t(rowptr, dev), dev_t(colidx, dev), dev_t(vals, dev), dev_t(B, dev)
+    if N == 1:
+        dC = torch.full((M, 1), float("nan"), device=dev)  # 4-byte rows
+    else:
+        ldc = N + 1 if (N + 1) % 4 else N + 2
+        dC = torch.full((M, ldc), float("nan"), device=dev)[:, :N]
+    capi.spmm(algo, drp, dci, dv, dB, dC, 1.0, 0.0)
+    torch.cuda.synchronize()
+    C = dC.cpu().numpy()
+    assert_parity(algo, C, rowptr, colidx, vals, B, None, 1.0, 0.0, what=f"split N={N}")
+
+
+@pytest.mark.parametrize("algo", ALGORITHMS)
 def test_empty_and_degenerate(algo, gpu):
     # nnz = 0 with beta != 0 and with beta == 0
     M, K, N = 50, 40, 12
