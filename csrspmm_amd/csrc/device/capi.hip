@@ -20,7 +20,7 @@ static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 WorkspaceLayout workspace_layout(int M, int K, int N, int nnz, int P) {
   WorkspaceLayout L{};
-  L.nslots = nnz / kSegLen;
+  L.nslots = nnz / kSlotLen;
   L.nblocks = merge_blocks(M, nnz, kMergeBlockMin);  // capacity for any merge block size
   L.ldp = ((long long)N + 3) & ~3LL;
   size_t off = 0;
@@ -29,7 +29,7 @@ WorkspaceLayout workspace_layout(int M, int K, int N, int nnz, int P) {
   L.seg_info_off = off;
   off = align256(off + (size_t)L.nslots * sizeof(int2));
   L.partials_off = off;
-  off = align256(off + (size_t)L.nslots * (size_t)L.ldp * sizeof(float));
+  off = align256(off + (size_t)(nnz / kSegLen) * (size_t)L.ldp * sizeof(float));
   L.base_total = off;
   if (P > 0 && K > 0) {
     const long long w = ((long long)K + P - 1) / P;
@@ -97,11 +97,11 @@ bool is_rowgroup(int algo) {
 }
 
 // The plan pays for itself on large matrices (short rows are streamed,
-// long rows split); small ones with no long row run as one launch.
+// long rows split); small ones with no row above kSegLen run as one launch.
 bool wants_plan(int algo, int M, int nnz, int hint) {
   if (!is_rowgroup(algo)) return false;
   if ((long long)M + nnz >= kPlanMinItems) return true;
-  return (hint < 0 || hint > kLongRow) && nnz > kLongRow;
+  return (hint < 0 || hint > kSegLen) && nnz > kSegLen;
 }
 
 int to_status(hipError_t e) { return e == hipSuccess ? 0 : (int)e; }

@@ -7,7 +7,7 @@
 //
 // Panelized rows.  A row of at least kPanelMinLen nonzeros with sorted
 // columns is cut at column-panel boundaries (P panels of K/P columns, the
-// B band of a panel is ~kPanelBandBytes) into pieces of at most kLongRow
+// B band of a panel is ~kPanelBandBytes) into pieces of at most kPieceMaxLen
 // nonzeros.  Panels are dealt to the 8 XCDs in column order, each to the
 // least-loaded XCD; the pieces of an XCD's panels, in panel order, form its
 // list, and each list is cut into units of ~kPanelUnitItems
@@ -115,8 +115,9 @@ hipError_t ensure_partials(csrspmm_plan_s* p, int N, hipStream_t s) {
   p->d_partials = p->d_pan_part = nullptr;
   p->ldp_cap = 0;
   p->partial_bytes = 0;
-  if (p->nslots > 0) {
-    e = hipMalloc(reinterpret_cast<void**>(&p->d_partials), (size_t)p->nslots * ldp * sizeof(float));
+  const size_t nparts = (size_t)(p->nnz / kSegLen);
+  if (nparts > 0) {
+    e = hipMalloc(reinterpret_cast<void**>(&p->d_partials), nparts * ldp * sizeof(float));
     if (e != hipSuccess) return e;
   }
   if (p->npieces > 0) {
@@ -124,7 +125,7 @@ hipError_t ensure_partials(csrspmm_plan_s* p, int N, hipStream_t s) {
     if (e != hipSuccess) return e;
   }
   p->ldp_cap = ldp;
-  p->partial_bytes = ((size_t)p->nslots + (size_t)p->npieces) * ldp * sizeof(float);
+  p->partial_bytes = (nparts + (size_t)p->npieces) * ldp * sizeof(float);
   return hipSuccess;
 }
 
@@ -136,9 +137,9 @@ int build_rowgroup_plan(csrspmm_plan_s* p, const std::vector<int>& rp, int n_hin
   int maxlen = 0;
   for (int r = 0; r < M; ++r) maxlen = std::max(maxlen, rp[r + 1] - rp[r]);
   p->maxlen = maxlen;
-  p->use_plan = ((long long)M + nnz >= kPlanMinItems) || maxlen > kLongRow;
+  p->use_plan = ((long long)M + nnz >= kPlanMinItems) || maxlen > kSegLen;
   if (!p->use_plan) return 0;
-  p->nslots = nnz / kSegLen;
+  p->nslots = nnz / kSlotLen;
   p->mblk = merge_block(vec);
   p->nblocks = merge_blocks(M, nnz, p->mblk);
 
@@ -179,9 +180,9 @@ int build_rowgroup_plan(csrspmm_plan_s* p, const std::vector<int>& rp, int n_hin
     fprev = f;
     if (r == M) break;
     const int len = rp[r + 1] - rp[r];
-    if (len > kLongRow && !panelized[r]) {
-      const int s0 = rp[r] / kSegLen;
-      for (int k = 0; k < len / kSegLen; ++k) seg_info[(size_t)s0 + k] = make_int2(r, k);
+    if (!panelized[r]) {
+      const int s0 = rp[r] / kSlotLen;
+      for (int k = 0; k < seg_count(len); ++k) seg_info[(size_t)s0 + k] = make_int2(r, k);
     }
   }
   block_start[(size_t)p->nblocks] = M;
@@ -190,7 +191,7 @@ int build_rowgroup_plan(csrspmm_plan_s* p, const std::vector<int>& rp, int n_hin
   if (e != hipSuccess) return (int)e;
   if (pan_rows.empty()) return 0;
 
-  // Pieces: (row index i, panel, [a, b)) with b - a <= kLongRow.
+  // Pieces: (row index i, panel, [a, b)) with b - a <= kPieceMaxLen.
   struct Piece {
     int i, a, b;
   };
@@ -202,7 +203,8 @@ int build_rowgroup_plan(csrspmm_plan_s* p, const std::vector<int>& rp, int n_hin
     for (int pn = 0; pn < P; ++pn) {
       const long long hi_col = (pn + 1) * width;
       const int b = (int)(std::lower_bound(hcol.begin() + a, hcol.begin() + rp[r + 1], (int)std::min<long long>(hi_col, 0x7fffffff)) - hcol.begin());
-      for (int x = a; x < b; x += kLongRow) by_panel[(size_t)pn].push_back({i, x, std::min(b, x + kLongRow)});
+      for (int x = a; x < b; x += kPieceMaxLen)
+        by_panel[(size_t)pn].push_back({i, x, std::min(b, x + kPieceMaxLen)});
       a = b;
     }
   }
@@ -217,9 +219,8 @@ int build_rowgroup_plan(csrspmm_plan_s* p, const std::vector<int>& rp, int n_hin
   }
   if (*std::max_element(weight.begin(), weight.end()) * P > kPanelSkewMax * total) {
     for (int r : pan_rows) {  // back to segments
-      const int len = rp[r + 1] - rp[r];
-      const int s0 = rp[r] / kSegLen;
-      for (int k = 0; k < len / kSegLen; ++k) seg_info[(size_t)s0 + k] = make_int2(r, k);
+      const int s0 = rp[r] / kSlotLen;
+      for (int k = 0; k < seg_count(rp[r + 1] - rp[r]); ++k) seg_info[(size_t)s0 + k] = make_int2(r, k);
     }
     return to_status(hipMemcpy(p->d_seg_info, seg_info.data(), seg_info.size() * sizeof(int2),
                                hipMemcpyHostToDevice));

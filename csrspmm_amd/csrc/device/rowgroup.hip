@@ -361,10 +361,12 @@ __device__ __forceinline__ void rowgroup_block(const Problem& p, int bid, int se
       const int re = p.rowptr[si.x + 1];
       const int len = re - rs;
       if (len >= kPanelMinLen && is_panelized(p, rs)) continue;  // summed by the pieces kernel
-      const int nseg = len / kSegLen;
+      const int nseg = seg_count(len);
       const int start = rs + seg_begin(len, nseg, si.y);
       const int end = rs + seg_begin(len, nseg, si.y + 1);
-      float* prow = p.partials + (long long)s * p.ldp;
+      // partial si.y of the row (si.y < the segments plan_kernel counted
+      // from the clamped row range, so this stays inside the buffer)
+      float* prow = p.partials + ((long long)(clamp_nnz(rs, p.nnz) / kSegLen) + si.y) * p.ldp;
       for (int c0 = c_lo; c0 < c_hi; c0 += PW) {
         const Panel<VEC, G, T> pn(p, c0, gl, c_hi);
         VT acc[T];
@@ -497,10 +499,9 @@ __global__ __launch_bounds__(256) void plan_kernel(Problem p) {
       } else {
         // slots [x0 / S, x1 / S) belong to row r; a long row uses the first nseg
         x1 = clamp_nnz(p.rowptr[r + 1], p.nnz);
-        s0 = x0 / kSegLen;
-        s1 = min(max(s0, x1 / kSegLen), p.nslots);
-        const int len = x1 - x0;
-        nseg = len > kLongRow ? len / kSegLen : 0;
+        s0 = x0 / kSlotLen;
+        s1 = min(max(s0, x1 / kSlotLen), p.nslots);
+        nseg = seg_count(x1 - x0);
         if (p.dp.P > 0) {
           // windows w whose first position w * kPanelMinLen lies in this row
           w0 = (x0 + kPanelMinLen - 1) / kPanelMinLen;
@@ -578,19 +579,20 @@ __device__ __forceinline__ void store_cols4(const Problem& p, float* cptr, int c
   }
 }
 
-// Segment slots one wave of the combine scan reads at once.  A split row
-// spans two slots or more, so a wave meets at most kScanSlots / 2 rows.
+// Table slots one wave of the combine scan reads at once.  A split row
+// (2 * kSegLen nonzeros or more) owns four slots or more, so a wave meets at
+// most kScanSlots / 4 rows to sum.
 constexpr int kScanSlots = 16;
 
 // C rows of split long rows (one partial per segment) and of panelized rows
 // (one partial per piece), each the sum of its partials in a fixed order, so
 // results repeat bit for bit.  A wave's lanes form P = 64 / GC groups of GC
 // lanes, each group covering 4 * GC columns (float4 per lane).
-//  * Blocks [0, scan_blocks): a wave reads kScanSlots consecutive segment
+//  * Blocks [0, scan_blocks): a wave reads kScanSlots consecutive table
 //    slots, loads the length of every row whose first segment lies among
-//    them (all at once), and sums the segments of each such row that has two
-//    or more: group q takes segments q, q + P, ..., then the P group sums
-//    meet in the xor tree.
+//    them (all at once), and sums the partials of each such row that has two
+//    segments or more: group q takes partials q, q + P, ..., then the P group
+//    sums meet in the xor tree.
 //  * Blocks [scan_blocks, ...): one panelized row per block.  Its 4 waves'
 //    4P groups split the pieces the same way; each wave's sum goes to LDS and
 //    wave 0 adds the four in wave order.
@@ -607,11 +609,11 @@ __global__ __launch_bounds__(kWaves * 64) void combine_kernel(Problem p, int sca
       const int s = ch * kScanSlots + lane;
       int2 si = make_int2(-1, 1);
       if (lane < kScanSlots && s < p.nslots) si = p.seg_info[s];
-      int nseg = 0;
+      int nseg = 0, x0 = 0;
       if (si.x >= 0 && si.x < p.M && si.y == 0) {
-        const int x0 = p.rowptr[si.x];
-        const int len = p.rowptr[si.x + 1] - x0;
-        nseg = len / kSegLen;
+        x0 = clamp_nnz(p.rowptr[si.x], p.nnz);
+        const int len = clamp_nnz(p.rowptr[si.x + 1], p.nnz) - x0;
+        nseg = seg_count(len);
         // one segment: stored by the segment phase; panelized: summed from pieces
         if (nseg < 2 || (len >= kPanelMinLen && is_panelized(p, x0))) nseg = 0;
       }
@@ -621,7 +623,8 @@ __global__ __launch_bounds__(kWaves * 64) void combine_kernel(Problem p, int sca
         rows &= rows - 1;
         const int row = __builtin_amdgcn_readlane(si.x, l);
         const int n = __builtin_amdgcn_readlane(nseg, l);
-        const float* base = p.partials + (long long)(ch * kScanSlots + l) * p.ldp;
+        // the row's partials x0 / kSegLen .. + n - 1
+        const float* base = p.partials + (long long)(__builtin_amdgcn_readlane(x0, l) / kSegLen) * p.ldp;
         float* crow = p.C + (long long)row * p.ldc;
         for (int c0 = 0; c0 < p.N; c0 += GC * 4) {
           const int c = c0 + gl * 4;
