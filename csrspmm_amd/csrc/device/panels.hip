@@ -18,8 +18,8 @@
 //  2. panel_sched_kernel, one workgroup: compacts the flagged rows into
 //     list[] in row order (at most nl_max of them; pidx[id] = their index,
 //     -1 elsewhere), gives XCD x the panels [x P / 8, (x + 1) P / 8), and
-//     estimates the panel loads from up to kDevPanelSample evenly spaced rows
-//     to turn panels off for this call when the heaviest panel carries more
+//     estimates the panel loads from up to kDevPanelSample rows (the first
+//     listed row in each of that many equal ranges of windows) to turn panels off for this call when the heaviest panel carries more
 //     than kPanelSkewMax times the mean (hot columns, as in R-MAT, already
 //     give L2 reuse) or the heaviest XCD range more than 1.5 times the mean.
 //
@@ -115,43 +115,64 @@ __global__ __launch_bounds__(kSchedThreads) void panel_sched_kernel(Problem p) {
   const int lane = lane_id();
   const int wave = t >> 6;
   constexpr int kWavesS = kSchedThreads / 64;
-  constexpr int kPer = 8;  // windows per thread per pass
+  constexpr int kPer = 16;  // windows per thread per pass
+  constexpr int kPass = kSchedThreads * kPer;
   __shared__ int s_wsum[kWavesS];
   __shared__ int s_base;
   __shared__ int s_id[kDevPanelSample];
   __shared__ int s_w[kPanelMaxPanels];
+  __shared__ unsigned char s_flag[kPass];
+  __shared__ int s_excl[kSchedThreads];
+  __shared__ unsigned s_mask[kSchedThreads];
   const int P = d.P;
 
-  // 1. Compaction of the flagged ids, in id (= row) order; thread t owns
-  // windows [k0 + kPer t, k0 + kPer (t + 1)).
+  // 1. Compaction of the flagged ids, in id (= row) order, kPass windows per
+  // pass.  The flags are read coalesced into LDS (window k0 + u * 1024 + t),
+  // thread t counts windows [k0 + kPer t, k0 + kPer (t + 1)) there, a block
+  // scan gives each thread its first list position, and pidx / list are
+  // written coalesced again, each window's position being its thread's
+  // start plus the flags before it in that thread's mask.  The sample for the
+  // panel loads is found on the way: the first listed id of each of
+  // kDevPanelSample equal ranges of window ids (LDS atomicMin, so the choice
+  // does not depend on timing).
   if (t == 0) s_base = 0;
   for (int q = t; q < P; q += kSchedThreads) s_w[q] = 0;
-  __syncthreads();
-  for (int k0 = 0; k0 < d.nwin; k0 += kSchedThreads * kPer) {
-    bool f[kPer];
-    int cnt = 0;
+  if (t < kDevPanelSample) s_id[t] = 0x7fffffff;
+  for (int k0 = 0; k0 < d.nwin; k0 += kPass) {
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
-      const int k = k0 + t * kPer + u;
-      f[u] = k < d.nwin && reinterpret_cast<const int*>(d.win + k)[3] == 1;
-      cnt += f[u] ? 1 : 0;
+      const int k = k0 + u * kSchedThreads + t;
+      s_flag[u * kSchedThreads + t] = k < d.nwin && reinterpret_cast<const int*>(d.win + k)[3] == 1;
     }
+    __syncthreads();
+    unsigned mask = 0;
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) mask |= (unsigned)s_flag[kPer * t + u] << u;
+    const int cnt = __builtin_popcount(mask);
     const int incl = wave_incl_scan(cnt, lane);
     if (lane == 63) s_wsum[wave] = incl;
     __syncthreads();
-    int i = s_base + incl - cnt;
-    for (int v = 0; v < wave; ++v) i += s_wsum[v];
+    int excl = s_base + incl - cnt;
+    for (int v = 0; v < wave; ++v) excl += s_wsum[v];
+    s_excl[t] = excl;
+    s_mask[t] = mask;
+    __syncthreads();
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
-      const int k = k0 + t * kPer + u;
+      const int j = u * kSchedThreads + t;  // window k0 + j, counted by thread j / kPer
+      const int k = k0 + j;
       if (k < d.nwin) {
-        const bool take = f[u] && i < d.nl_max;
+        const unsigned m = s_mask[j / kPer];
+        const int bit = j % kPer;
+        const int i = s_excl[j / kPer] + __builtin_popcount(m & ((1u << bit) - 1u));
+        const bool take = ((m >> bit) & 1u) && i < d.nl_max;
         d.pidx[k] = take ? i : -1;
-        if (take) d.list[i] = k;
+        if (take) {
+          d.list[i] = k;
+          atomicMin(&s_id[(int)(((long long)k * kDevPanelSample) / d.nwin)], k);
+        }
       }
-      i += f[u] ? 1 : 0;
     }
-    __syncthreads();
     if (t == 0) {
       int tot = 0;
       for (int v = 0; v < kWavesS; ++v) tot += s_wsum[v];
@@ -161,20 +182,18 @@ __global__ __launch_bounds__(kSchedThreads) void panel_sched_kernel(Problem p) {
   }
   const int nl = min(s_base, d.nl_max);
 
-  // 2. Panel loads from ns <= kDevPanelSample evenly spaced rows: pair
-  // m = (sample m / P, panel m % P), all loads of a thread in flight at once.
-  const int ns = min(nl, kDevPanelSample);
-  if (t < ns) s_id[t] = d.list[(int)(((long long)t * nl) / ns)];
-  __syncthreads();
+  // 2. Panel loads of the sampled rows: pair m = (sample m / P, panel m % P),
+  // all loads of a thread in flight at once (empty ranges have no sample).
   constexpr int kPairs = kDevPanelSample * kPanelMaxPanels / kSchedThreads;
-  const int npairs = ns * P;
+  const int npairs = kDevPanelSample * P;
   int b0[kPairs], b1[kPairs];
 #pragma unroll
   for (int u = 0; u < kPairs; ++u) {
     const int m = t + u * kSchedThreads;
     b0[u] = b1[u] = 0;
-    if (m < npairs) {
-      const int* b = d.bnd + (long long)s_id[m / P] * (P + 1) + (m % P);
+    const int id = m < npairs ? s_id[m / P] : 0x7fffffff;
+    if (id != 0x7fffffff) {
+      const int* b = d.bnd + (long long)id * (P + 1) + (m % P);
       b0[u] = b[0];
       b1[u] = b[1];
     }
