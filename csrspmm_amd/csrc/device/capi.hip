@@ -254,6 +254,7 @@ int spmm_impl(int algo_in, int M, int K, int N, int nnz, const int* rowptr, cons
       if (ws_bytes < L.total) L = workspace_layout(M, K, N, nnz, 0);
     }
     bind_workspace(p, ws, L, merge_block(vec));
+    set_row_hint(p, hint);
   }
   return to_status(launch_algorithm(algo, p, s));
 }

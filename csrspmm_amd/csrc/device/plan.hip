@@ -115,7 +115,8 @@ hipError_t ensure_partials(csrspmm_plan_s* p, int N, hipStream_t s) {
   p->d_partials = p->d_pan_part = nullptr;
   p->ldp_cap = 0;
   p->partial_bytes = 0;
-  const size_t nparts = (size_t)(p->nnz / kSegLen);
+  // partials only for rows of two segments or more
+  const size_t nparts = p->maxlen < 2 * kSegLen ? 0 : (size_t)(p->nnz / kSegLen);
   if (nparts > 0) {
     e = hipMalloc(reinterpret_cast<void**>(&p->d_partials), nparts * ldp * sizeof(float));
     if (e != hipSuccess) return e;
@@ -139,7 +140,7 @@ int build_rowgroup_plan(csrspmm_plan_s* p, const std::vector<int>& rp, int n_hin
   p->maxlen = maxlen;
   p->use_plan = ((long long)M + nnz >= kPlanMinItems) || maxlen > kSegLen;
   if (!p->use_plan) return 0;
-  p->nslots = nnz / kSlotLen;
+  p->nslots = maxlen <= kLongRow ? 0 : nnz / kSlotLen;  // no long row: no segment table
   p->mblk = merge_block(vec);
   p->nblocks = merge_blocks(M, nnz, p->mblk);
 
@@ -370,6 +371,7 @@ int csrspmm_plan_spmm_f32(csrspmm_plan_t plan, int N, const float* B, long long 
   pr.plan = true;
   pr.plan_ready = true;
   pr.nslots = p->nslots;
+  set_row_hint(pr, p->maxlen);
   pr.mblk = p->mblk;
   pr.nblocks = p->nblocks;
   pr.block_start = p->d_block_start;
@@ -404,6 +406,8 @@ int csrspmm_plan_spmm_f32(csrspmm_plan_t plan, int N, const float* B, long long 
     d.block_start = p->d_unit_start;
     d.nslots = 0;
     d.npan = 0;
+    d.rows_whole = true;  // pieces hold at most kPieceMaxLen <= kLongRow nonzeros
+    d.no_split = true;
     e = launch_rowgroup(d, vec, lds, s);
   }
   if (e == hipSuccess) e = launch_rowgroup(pr, vec, lds, s);

@@ -220,7 +220,7 @@ __device__ __forceinline__ void stream_rows(const Problem& p, const Panel<VEC, G
       lo = p.rowptr[rs + gl];
       hi = p.rowptr[rs + gl + 1];
     }
-    const bool is_long = gl < nbm && (hi - lo) > kLongRow;
+    const bool is_long = gl < nbm && !p.rows_whole && (hi - lo) > kLongRow;
     const unsigned long long bl = __ballot(is_long) & gmask;
     const int nb = bl ? (__ffsll((long long)bl) - 1 - gbase) : nbm;  // rows before the first long one
     if (nb > 0) {
@@ -361,7 +361,7 @@ __device__ __forceinline__ void rowgroup_block(const Problem& p, int bid, int se
       const int re = p.rowptr[si.x + 1];
       const int len = re - rs;
       if (len >= kPanelMinLen && is_panelized(p, rs)) continue;  // summed by the pieces kernel
-      const int nseg = seg_count(len);
+      const int nseg = seg_count(p, len);
       const int start = rs + seg_begin(len, nseg, si.y);
       const int end = rs + seg_begin(len, nseg, si.y + 1);
       // partial si.y of the row (si.y < the segments plan_kernel counted
@@ -501,7 +501,7 @@ __global__ __launch_bounds__(256) void plan_kernel(Problem p) {
         x1 = clamp_nnz(p.rowptr[r + 1], p.nnz);
         s0 = x0 / kSlotLen;
         s1 = min(max(s0, x1 / kSlotLen), p.nslots);
-        nseg = seg_count(x1 - x0);
+        nseg = seg_count(p, x1 - x0);
         if (p.dp.P > 0) {
           // windows w whose first position w * kPanelMinLen lies in this row
           w0 = (x0 + kPanelMinLen - 1) / kPanelMinLen;
@@ -613,7 +613,7 @@ __global__ __launch_bounds__(kWaves * 64) void combine_kernel(Problem p, int sca
       if (si.x >= 0 && si.x < p.M && si.y == 0) {
         x0 = clamp_nnz(p.rowptr[si.x], p.nnz);
         const int len = clamp_nnz(p.rowptr[si.x + 1], p.nnz) - x0;
-        nseg = seg_count(len);
+        nseg = seg_count(p, len);
         // one segment: stored by the segment phase; panelized: summed from pieces
         if (nseg < 2 || (len >= kPanelMinLen && is_panelized(p, x0))) nseg = 0;
       }
@@ -791,7 +791,7 @@ static hipError_t launch_rowgroup_all(const Problem& p, int vec, bool lds, hipSt
     e = lds ? dispatch_vec1<true>(p, s) : dispatch_vec1<false>(p, s);
   }
   if (e != hipSuccess) return e;
-  if (p.plan && (p.nslots + p.npan > 0 || p.dp.P > 0)) {
+  if (p.plan && ((p.nslots > 0 && !p.no_split) || p.npan > 0 || p.dp.P > 0)) {
     if (vec == 4) {
       launch_combine<4>(p, s);
     } else {

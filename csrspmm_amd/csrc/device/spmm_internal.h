@@ -245,7 +245,27 @@ struct Problem {
   // Slices as one launch each (true) or all in one launch, slice after slice
   // in block order (false).
   bool slice_launch;
+  // From the caller's max_row_nnz hint (or a stored plan's true maximum):
+  // rows_whole, no row above kLongRow: no segment phase (nslots = 0) and the
+  // merge blocks sum every row whole, whatever its length, so a hint that is
+  // too small costs time, never correctness; no_split, no row of 2 * kSegLen
+  // nonzeros: a long row is one segment, so no partials and no combine.
+  bool rows_whole;
+  bool no_split;
 };
+
+// Segments of a row of len nonzeros under the problem's hint.
+__host__ __device__ inline int seg_count(const Problem& p, int len) {
+  const int n = seg_count(len);
+  return p.no_split && n > 1 ? 1 : n;
+}
+
+// The hint flags for a longest row of max_row_nnz nonzeros (-1: unknown).
+inline void set_row_hint(Problem& p, int max_row_nnz) {
+  p.rows_whole = max_row_nnz >= 0 && max_row_nnz <= kLongRow;
+  p.no_split = max_row_nnz >= 0 && max_row_nnz < 2 * kSegLen;
+  if (p.rows_whole) p.nslots = 0;
+}
 
 // Workspace layout for a problem (all offsets 256-byte aligned).  P > 0 adds
 // the per-call panel tables and partial buffer after the base sections.

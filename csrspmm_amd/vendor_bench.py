@@ -103,6 +103,15 @@ def main(argv=None):
         ms = timed(torch, lambda: capi.spmm("Auto", rp, ci, va, dB, ours_C, 1.0, 0.0, workspace=ws),
                    args.reps)
         row("csrspmm Auto (per call)", ms, None)
+        # with max_row_nnz, which a reference CSRMatrix carries (csrspmm::spmm passes it)
+        mr = int((a.rowptr[1:] - a.rowptr[:-1]).max()) if a.M else 0
+        ws_h = torch.empty(max(capi.hip().csrspmm_workspace_bytes_ex(capi.ALGO["Auto"], a.M, a.K, N, a.nnz, mr),
+                               1), dtype=torch.uint8, device=dev)
+        Ch = torch.empty_like(ours_C)
+        ms = timed(torch, lambda: capi.spmm("Auto", rp, ci, va, dB, Ch, 1.0, 0.0, workspace=ws_h, hint=mr),
+                   args.reps)
+        row("csrspmm Auto (per call, max_row_nnz given)", ms, Ch)
+        del Ch, ws_h
         plan = capi.Plan("Auto", rp, ci, va, a.K, n_hint=N)
         Cp = torch.empty_like(ours_C)
         ms = timed(torch, lambda: plan.spmm(dB, Cp, 1.0, 0.0), args.reps)

@@ -87,8 +87,8 @@ size_t csrspmm_workspace_bytes(int algo, int M, int N, int nnz);
 /* As csrspmm_workspace_bytes, plus the per-call column-panel tables and
  * partial sums that float4 variants use for rows of >= 1024 nonzeros when B
  * (K x N fp32) is >= 16 MiB and N <= 256 (at most 256 MiB of partials).  A
- * max_row_nnz_hint in [0, 1024) tells that no such row exists (-1: unknown)
- * exists.  csrspmm_spmm_f32_ex given a workspace of at least
+ * max_row_nnz_hint in [0, 1024) tells that no such row exists (-1: unknown).
+ * csrspmm_spmm_f32_ex given a workspace of at least
  * csrspmm_workspace_bytes but less than this size runs without panels. */
 size_t csrspmm_workspace_bytes_ex(int algo, int M, int K, int N, int nnz, int max_row_nnz_hint);
 
@@ -100,9 +100,13 @@ size_t csrspmm_workspace_bytes_ex(int algo, int M, int K, int N, int nnz, int ma
  *   M, K, N, nnz    A is M x K with nnz nonzeros; B is K x N; C is M x N
  *   rowptr, colidx, vals   device CSR arrays (M+1, nnz, nnz entries)
  *   max_row_nnz_hint       -1 if unknown; otherwise the caller's claim of the
- *                   longest row.  Used only to skip the row-split plan when
- *                   every row is short; never used to size memory, so a
- *                   wrong hint costs speed, not safety.
+ *                   longest row.  It only steers the plan: at most 128 drops
+ *                   the long-row segments and their combine pass, below 512
+ *                   the split rows and the combine, below 1024 the column
+ *                   panels, and a small matrix with no row above 256 runs as
+ *                   one launch.  Never used to size memory or bound a loop:
+ *                   a hint below the true longest row still gives the exact
+ *                   result, only more slowly.
  *   B, ldb, C, ldc  row-major dense operands, ldb >= N, ldc >= N
  *   stream          hipStream_t (NULL = legacy default stream)
  * Asynchronous: returns after enqueueing.  Uses a library-owned device

@@ -187,6 +187,30 @@ def test_strided_b_and_split_boundaries(algo, gpu):
     assert_parity(algo, C, rowptr, colidx, vals, Bfull[:, :N].copy(), None, 1.0, 0.0, what="strided")
 
 
+@pytest.mark.parametrize("algo", ["WarpPerRow", "WarpPerRowFp4", "WarpPerRowSmem", "WarpPerRowSmemFp4"])
+@pytest.mark.parametrize("hint", [-1, 60, 128, 300, 2000, 5000])
+def test_row_hint(algo, hint, gpu):
+    """The max_row_nnz hint only steers the plan: at most 128 drops the
+    segment phase (the merge blocks sum every row whole), below 512 drops
+    split rows (one segment per long row).  A hint below the true longest
+    row (2000 here) gives the right result, only slower."""
+    rng = np.random.default_rng(7)
+    K = 6000
+    short = rng.integers(0, 6, 30000)
+    long_ = np.array([100, 129, 200, 255, 256, 400, 511, 512, 600, 1200, 2000])
+    lens = short.copy()
+    lens[rng.choice(lens.size, long_.size, replace=False)] = long_
+    rowptr = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    colidx = np.concatenate([np.sort(rng.choice(K, L, replace=False)) for L in lens]).astype(np.int32)
+    vals = rng.uniform(-1, 1, colidx.size).astype(np.float32)
+    B = rng.uniform(-1, 1, (K, 64)).astype(np.float32)
+    C = run_spmm(algo, rowptr, colidx, vals, B, gpu, hint=hint)
+    assert_parity(algo, C, rowptr, colidx, vals, B, None, 1.0, 0.0, what=f"hint={hint}")
+    C0 = rng.uniform(-1, 1, (lens.size, 64)).astype(np.float32)
+    C = run_spmm(algo, rowptr, colidx, vals, B, gpu, C0=C0, alpha=0.5, beta=2.0, hint=hint)
+    assert_parity(algo, C, rowptr, colidx, vals, B, C0, 0.5, 2.0, what=f"hint={hint} beta")
+
+
 @pytest.mark.parametrize("algo", ALGORITHMS)
 @pytest.mark.parametrize("N", [1, 3, 5, 130])
 def test_split_rows_odd_columns(algo, N, gpu):
