@@ -21,7 +21,8 @@ static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 WorkspaceLayout workspace_layout(int M, int K, int N, int nnz, int P) {
   WorkspaceLayout L{};
   L.nslots = nnz / kSlotLen;
-  L.nblocks = merge_blocks(M, nnz, kMergeBlockMin);  // capacity for any merge block size
+  // capacity for the merge blocks of either column width
+  L.nblocks = merge_blocks(M, nnz, std::min(merge_block(1, M, nnz), merge_block(4, M, nnz)));
   L.ldp = ((long long)N + 3) & ~3LL;
   size_t off = 0;
   L.block_start_off = off;
@@ -253,7 +254,7 @@ int spmm_impl(int algo_in, int M, int K, int N, int nnz, const int* rowptr, cons
       // a workspace sized without the panel tables runs without panels
       if (ws_bytes < L.total) L = workspace_layout(M, K, N, nnz, 0);
     }
-    bind_workspace(p, ws, L, merge_block(vec));
+    bind_workspace(p, ws, L, merge_block(vec, M, nnz));
     set_row_hint(p, hint);
   }
   return to_status(launch_algorithm(algo, p, s));

@@ -141,7 +141,7 @@ int build_rowgroup_plan(csrspmm_plan_s* p, const std::vector<int>& rp, int n_hin
   p->use_plan = ((long long)M + nnz >= kPlanMinItems) || maxlen > kSegLen;
   if (!p->use_plan) return 0;
   p->nslots = maxlen <= kLongRow ? 0 : nnz / kSlotLen;  // no long row: no segment table
-  p->mblk = merge_block(vec);
+  p->mblk = merge_block(vec, M, nnz);
   p->nblocks = merge_blocks(M, nnz, p->mblk);
 
   // Panelized rows: long, on a large B, with non-decreasing columns.

@@ -83,11 +83,19 @@ static_assert(kPieceMaxLen <= kLongRow, "pieces are streamed as short rows");
 #endif
 constexpr int kMergeBlock = CSRSPMM_MERGE_BLOCK;
 constexpr int kMergeBlockVec4 = CSRSPMM_MERGE_BLOCK_VEC4;
-constexpr int kMergeBlockMin = kMergeBlock < kMergeBlockVec4 ? kMergeBlock : kMergeBlockVec4;
 constexpr int kMergeBlockMax = kMergeBlock > kMergeBlockVec4 ? kMergeBlock : kMergeBlockVec4;
 static_assert((kMergeBlock & (kMergeBlock - 1)) == 0 && (kMergeBlockVec4 & (kMergeBlockVec4 - 1)) == 0,
               "merge blocks are powers of two (plan_kernel shifts by them)");
-inline int merge_block(int vec) { return vec == 4 ? kMergeBlockVec4 : kMergeBlock; }
+// A small problem gets smaller merge blocks, down to one item, so that it
+// still has at least kMinMergeBlocks of them to spread over the GPU's
+// 256 CUs (measured on MI355X: 512 rows x N = 1024 with the full block ran
+// as 7 groups, 187 us a call).
+constexpr long long kMinMergeBlocks = 4096;
+inline int merge_block(int vec, int M, int nnz) {
+  int m = vec == 4 ? kMergeBlockVec4 : kMergeBlock;
+  while (m > 1 && ((long long)M + nnz + 1) / m < kMinMergeBlocks) m >>= 1;
+  return m;
+}
 inline int merge_blocks(int M, int nnz, int mblk) {
   return (int)(((long long)M + nnz + 1 + mblk - 1) / mblk);
 }
