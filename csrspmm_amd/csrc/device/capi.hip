@@ -20,7 +20,8 @@ static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 WorkspaceLayout workspace_layout(int M, int K, int N, int nnz, int P) {
   WorkspaceLayout L{};
-  L.nslots = nnz / kSlotLen;
+  const SegGeom g = seg_geom(nnz);
+  L.nslots = nnz >> g.slot_shift;
   // capacity for the merge blocks of either column width
   L.nblocks = merge_blocks(M, nnz, std::min(merge_block(1, M, nnz), merge_block(4, M, nnz)));
   L.ldp = ((long long)N + 3) & ~3LL;
@@ -30,7 +31,7 @@ WorkspaceLayout workspace_layout(int M, int K, int N, int nnz, int P) {
   L.seg_info_off = off;
   off = align256(off + (size_t)L.nslots * sizeof(int2));
   L.partials_off = off;
-  off = align256(off + (size_t)(nnz / kSegLen) * (size_t)L.ldp * sizeof(float));
+  off = align256(off + (size_t)(nnz >> g.seg_shift) * (size_t)L.ldp * sizeof(float));
   L.base_total = off;
   if (P > 0 && K > 0) {
     const long long w = ((long long)K + P - 1) / P;
@@ -185,6 +186,10 @@ int fill_problem(Problem& p, int algo, int M, int K, int N, int nnz, const int* 
   p.K = K;
   p.N = N;
   p.nnz = nnz;
+  const SegGeom g = seg_geom(nnz);
+  p.seg_shift = g.seg_shift;
+  p.slot_shift = g.slot_shift;
+  p.long_row = g.long_row;
   if (M == 0 || N == 0) return 0;
   if (!rowptr || !C) return CSRSPMM_STATUS_INVALID_VALUE;
   if (nnz > 0 && (!colidx || !vals || !B || K == 0)) return CSRSPMM_STATUS_INVALID_VALUE;

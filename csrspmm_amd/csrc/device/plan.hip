@@ -116,7 +116,8 @@ hipError_t ensure_partials(csrspmm_plan_s* p, int N, hipStream_t s) {
   p->ldp_cap = 0;
   p->partial_bytes = 0;
   // partials only for rows of two segments or more
-  const size_t nparts = p->maxlen < 2 * kSegLen ? 0 : (size_t)(p->nnz / kSegLen);
+  const SegGeom g = seg_geom(p->nnz);
+  const size_t nparts = p->maxlen < (2 << g.seg_shift) ? 0 : (size_t)(p->nnz >> g.seg_shift);
   if (nparts > 0) {
     e = hipMalloc(reinterpret_cast<void**>(&p->d_partials), nparts * ldp * sizeof(float));
     if (e != hipSuccess) return e;
@@ -140,7 +141,8 @@ int build_rowgroup_plan(csrspmm_plan_s* p, const std::vector<int>& rp, int n_hin
   p->maxlen = maxlen;
   p->use_plan = ((long long)M + nnz >= kPlanMinItems) || maxlen > kSegLen;
   if (!p->use_plan) return 0;
-  p->nslots = maxlen <= kLongRow ? 0 : nnz / kSlotLen;  // no long row: no segment table
+  const SegGeom g = seg_geom(nnz);
+  p->nslots = maxlen <= g.long_row ? 0 : nnz >> g.slot_shift;  // no long row: no segment table
   p->mblk = merge_block(vec, M, nnz);
   p->nblocks = merge_blocks(M, nnz, p->mblk);
 
@@ -182,8 +184,9 @@ int build_rowgroup_plan(csrspmm_plan_s* p, const std::vector<int>& rp, int n_hin
     if (r == M) break;
     const int len = rp[r + 1] - rp[r];
     if (!panelized[r]) {
-      const int s0 = rp[r] / kSlotLen;
-      for (int k = 0; k < seg_count(len); ++k) seg_info[(size_t)s0 + k] = make_int2(r, k);
+      const int s0 = rp[r] >> g.slot_shift;
+      for (int k = 0; k < seg_count(len, g.long_row, g.seg_shift); ++k)
+        seg_info[(size_t)s0 + k] = make_int2(r, k);
     }
   }
   block_start[(size_t)p->nblocks] = M;
@@ -220,8 +223,9 @@ int build_rowgroup_plan(csrspmm_plan_s* p, const std::vector<int>& rp, int n_hin
   }
   if (*std::max_element(weight.begin(), weight.end()) * P > kPanelSkewMax * total) {
     for (int r : pan_rows) {  // back to segments
-      const int s0 = rp[r] / kSlotLen;
-      for (int k = 0; k < seg_count(rp[r + 1] - rp[r]); ++k) seg_info[(size_t)s0 + k] = make_int2(r, k);
+      const int s0 = rp[r] >> g.slot_shift;
+      for (int k = 0; k < seg_count(rp[r + 1] - rp[r], g.long_row, g.seg_shift); ++k)
+        seg_info[(size_t)s0 + k] = make_int2(r, k);
     }
     return to_status(hipMemcpy(p->d_seg_info, seg_info.data(), seg_info.size() * sizeof(int2),
                                hipMemcpyHostToDevice));
@@ -406,7 +410,7 @@ int csrspmm_plan_spmm_f32(csrspmm_plan_t plan, int N, const float* B, long long 
     d.block_start = p->d_unit_start;
     d.nslots = 0;
     d.npan = 0;
-    d.rows_whole = true;  // pieces hold at most kPieceMaxLen <= kLongRow nonzeros
+    d.rows_whole = true;  // pieces (at most kPieceMaxLen nonzeros) are summed whole
     d.no_split = true;
     e = launch_rowgroup(d, vec, lds, s);
   }

@@ -220,7 +220,7 @@ __device__ __forceinline__ void stream_rows(const Problem& p, const Panel<VEC, G
       lo = p.rowptr[rs + gl];
       hi = p.rowptr[rs + gl + 1];
     }
-    const bool is_long = gl < nbm && !p.rows_whole && (hi - lo) > kLongRow;
+    const bool is_long = gl < nbm && !p.rows_whole && (hi - lo) > p.long_row;
     const unsigned long long bl = __ballot(is_long) & gmask;
     const int nb = bl ? (__ffsll((long long)bl) - 1 - gbase) : nbm;  // rows before the first long one
     if (nb > 0) {
@@ -366,7 +366,7 @@ __device__ __forceinline__ void rowgroup_block(const Problem& p, int bid, int se
       const int end = rs + seg_begin(len, nseg, si.y + 1);
       // partial si.y of the row (si.y < the segments plan_kernel counted
       // from the clamped row range, so this stays inside the buffer)
-      float* prow = p.partials + ((long long)(clamp_nnz(rs, p.nnz) / kSegLen) + si.y) * p.ldp;
+      float* prow = p.partials + ((long long)(clamp_nnz(rs, p.nnz) >> p.seg_shift) + si.y) * p.ldp;
       for (int c0 = c_lo; c0 < c_hi; c0 += PW) {
         const Panel<VEC, G, T> pn(p, c0, gl, c_hi);
         VT acc[T];
@@ -470,10 +470,14 @@ __device__ __forceinline__ void plan_row_entries(const Problem& p, int r, int b_
 }
 
 // A row with more table entries than this has them written by its whole
-// wave, 64 per store instruction, instead of by its own lane one at a time
-// (a long row covers hundreds of merge blocks, and one lane can hold only a
-// few dozen stores in flight).
-constexpr int kPlanSoloEntries = 8;
+// wave, 64 per store instruction, instead of by its own lane one at a time:
+// a long row covers hundreds of merge blocks, and one lane holds at most 63
+// stores in flight.  Below it, the lanes write their rows in parallel (the
+// wave-wide path takes the rows one after another).
+#ifndef CSRSPMM_PLAN_SOLO_ENTRIES
+#define CSRSPMM_PLAN_SOLO_ENTRIES 32
+#endif
+constexpr int kPlanSoloEntries = CSRSPMM_PLAN_SOLO_ENTRIES;
 
 // One thread per row r in [0, M]: the merge-block starts that fall on r, the
 // segment slots r owns and, with column panels, the windows that begin in r.
@@ -499,8 +503,8 @@ __global__ __launch_bounds__(256) void plan_kernel(Problem p) {
       } else {
         // slots [x0 / S, x1 / S) belong to row r; a long row uses the first nseg
         x1 = clamp_nnz(p.rowptr[r + 1], p.nnz);
-        s0 = x0 / kSlotLen;
-        s1 = min(max(s0, x1 / kSlotLen), p.nslots);
+        s0 = x0 >> p.slot_shift;
+        s1 = min(max(s0, x1 >> p.slot_shift), p.nslots);
         nseg = seg_count(p, x1 - x0);
         if (p.dp.P > 0) {
           // windows w whose first position w * kPanelMinLen lies in this row
@@ -579,9 +583,9 @@ __device__ __forceinline__ void store_cols4(const Problem& p, float* cptr, int c
   }
 }
 
-// Table slots one wave of the combine scan reads at once.  A split row
-// (2 * kSegLen nonzeros or more) owns four slots or more, so a wave meets at
-// most kScanSlots / 4 rows to sum.
+// Table slots one wave of the combine scan reads at once.  A split row (two
+// segments or more) owns two slots or more, so a wave meets at most
+// kScanSlots / 2 rows to sum.
 constexpr int kScanSlots = 16;
 
 // C rows of split long rows (one partial per segment) and of panelized rows
@@ -624,7 +628,7 @@ __global__ __launch_bounds__(kWaves * 64) void combine_kernel(Problem p, int sca
         const int row = __builtin_amdgcn_readlane(si.x, l);
         const int n = __builtin_amdgcn_readlane(nseg, l);
         // the row's partials x0 / kSegLen .. + n - 1
-        const float* base = p.partials + (long long)(__builtin_amdgcn_readlane(x0, l) / kSegLen) * p.ldp;
+        const float* base = p.partials + (long long)(__builtin_amdgcn_readlane(x0, l) >> p.seg_shift) * p.ldp;
         float* crow = p.C + (long long)row * p.ldc;
         for (int c0 = 0; c0 < p.N; c0 += GC * 4) {
           const int c = c0 + gl * 4;

@@ -18,25 +18,31 @@ enum EpilogueMode : int {
                        // it (the torch forwards' zeros()+beta, torch_csrspmm_naive.cpp:32-34)
 };
 
-// Long rows.  A row of len > kLongRow nonzeros leaves the merge blocks of
-// short rows and is cut into nseg = max(1, floor(len / kSegLen)) segments
-// of near-equal length: segment k covers nonzeros
+// Long rows.  A row of len > long_row nonzeros leaves the merge blocks of
+// short rows and is cut into nseg = max(1, floor(len / seg)) segments of
+// near-equal length: segment k covers nonzeros
 // [seg_begin(len, nseg, k), seg_begin(len, nseg, k + 1)) of the row, so a
-// row's segments differ in length by at most one (up to 2*kSegLen-1
-// nonzeros for a single segment, at most (3/2)*kSegLen from two on).  A row
-// with one segment is summed whole and stored with the epilogue directly;
-// otherwise segment k's partial sum goes to workspace partial
-// rowptr[r] / kSegLen + k, and a combine pass adds the partials of the row
-// in segment order and applies the epilogue.  The segments run in the first
-// blocks of the main launch, so rows of kLongRow+ nonzeros, each one group's
-// chain of dependent gathers, start early rather than trailing the short
-// rows (measured on MI355X: kLongRow 128 instead of 256, 2.5% faster on XL).
+// row's segments differ in length by at most one (up to 2*seg-1 nonzeros for
+// a single segment, at most (3/2)*seg from two on).  A row with one segment is
+// summed whole and stored with the epilogue directly; otherwise segment k's
+// partial sum goes to workspace partial rowptr[r] / seg + k, and a combine
+// pass adds the partials of the row in segment order and applies the
+// epilogue.  The segments run in the first blocks of the main launch, so
+// rows above long_row, each one group's chain of dependent gathers, start
+// early rather than trailing the short rows (measured on MI355X: long_row
+// 128 instead of 256, 2.5% faster on XL).
 //
 // No counters are needed: row r owns the table slots
-// [rowptr[r] / kSlotLen, rowptr[r+1] / kSlotLen), at least one for
-// len > kLongRow >= kSlotLen and at least nseg, and the partials
-// [rowptr[r] / kSegLen, rowptr[r+1] / kSegLen), at least nseg when nseg >= 2;
-// the ranges of all rows tile [0, nnz / kSlotLen) and [0, nnz / kSegLen).
+// [rowptr[r] / slot, rowptr[r+1] / slot), at least one for
+// len > long_row >= slot and at least nseg since seg >= slot, and the
+// partials [rowptr[r] / seg, rowptr[r+1] / seg), at least nseg when
+// nseg >= 2; the ranges of all rows tile [0, nnz / slot) and [0, nnz / seg).
+//
+// The geometry (seg, slot, long_row) is (kSegLen, kSlotLen, kLongRow), or,
+// for a matrix with fewer than kMinSegments * kSegLen nonzeros, seg halved
+// down to kSegLenMin until there are kMinSegments segments' worth of
+// nonzeros, with slot and long_row at most seg: a small matrix's long rows
+// still split into enough chains to fill the GPU.
 #ifndef CSRSPMM_SEG_LEN
 #define CSRSPMM_SEG_LEN 256
 #endif
@@ -49,13 +55,36 @@ enum EpilogueMode : int {
 constexpr int kSegLen = CSRSPMM_SEG_LEN;
 constexpr int kLongRow = CSRSPMM_LONG_ROW;
 constexpr int kSlotLen = CSRSPMM_SLOT_LEN;
+constexpr int kSegLenMin = 32;
+constexpr long long kMinSegments = 4096;
 static_assert(kLongRow >= kSlotLen, "a long row owns at least one table slot");
 static_assert(kSegLen >= kSlotLen, "a row owns a table slot for each of its segments");
+static_assert((kSegLen & (kSegLen - 1)) == 0 && (kSlotLen & (kSlotLen - 1)) == 0 &&
+                  kSegLenMin <= kSlotLen && kSegLenMin <= kLongRow,
+              "segment geometry: powers of two, shortened down to kSegLenMin");
+
+struct SegGeom {
+  int seg_shift;   // seg = 1 << seg_shift
+  int slot_shift;  // slot = 1 << slot_shift
+  int long_row;
+};
+
+inline SegGeom seg_geom(int nnz) {
+  int seg = kSegLen;
+  while (seg > kSegLenMin && (long long)nnz / seg < kMinSegments) seg >>= 1;
+  const int slot = seg < kSlotLen ? seg : kSlotLen;
+  SegGeom g;
+  g.seg_shift = __builtin_ctz((unsigned)seg);
+  g.slot_shift = __builtin_ctz((unsigned)slot);
+  g.long_row = seg < kLongRow ? seg : kLongRow;
+  return g;
+}
 
 // Segments of a row of len nonzeros (0: a short row).
-__host__ __device__ inline int seg_count(int len) {
-  if (len <= kLongRow) return 0;
-  return len < 2 * kSegLen ? 1 : len / kSegLen;
+__host__ __device__ inline int seg_count(int len, int long_row, int seg_shift) {
+  if (len <= long_row) return 0;
+  const int n = len >> seg_shift;
+  return n < 2 ? 1 : n;
 }
 
 __host__ __device__ inline int seg_begin(int len, int nseg, int k) {
@@ -226,12 +255,12 @@ struct Problem {
   // Plan (all inside the workspace, all written by plan_kernel each call).
   // plan == false: every row is processed whole by its own group.
   bool plan;
-  int nslots;         // table slots, nnz / kSlotLen
+  int nslots;         // table slots, nnz / slot
   int mblk;           // merge block size (rows + nonzeros)
   int nblocks;        // merge blocks
   int* block_start;   // nblocks + 1 entries: first row of each merge block, then M
   int2* seg_info;     // per slot: (row, segment index) or (-1, 0) for an unused slot
-  float* partials;    // nnz / kSegLen partial rows of ldp floats
+  float* partials;    // nnz / seg partial rows of ldp floats
   long long ldp;
   // A stored plan (csrspmm_plan_create) filled block_start / seg_info once:
   // no plan_kernel launch per call.
@@ -260,18 +289,22 @@ struct Problem {
   // nonzeros: a long row is one segment, so no partials and no combine.
   bool rows_whole;
   bool no_split;
+  // Segment geometry (seg_geom).  New fields go here, at the end: inserting
+  // them above shifted the kernel-argument offsets of the fields after them
+  // and, with the same kernel code, measured 4-5% slower on the XL configs.
+  int seg_shift, slot_shift, long_row;
 };
 
-// Segments of a row of len nonzeros under the problem's hint.
+// Segments of a row of len nonzeros under the problem's geometry and hint.
 __host__ __device__ inline int seg_count(const Problem& p, int len) {
-  const int n = seg_count(len);
+  const int n = seg_count(len, p.long_row, p.seg_shift);
   return p.no_split && n > 1 ? 1 : n;
 }
 
 // The hint flags for a longest row of max_row_nnz nonzeros (-1: unknown).
 inline void set_row_hint(Problem& p, int max_row_nnz) {
-  p.rows_whole = max_row_nnz >= 0 && max_row_nnz <= kLongRow;
-  p.no_split = max_row_nnz >= 0 && max_row_nnz < 2 * kSegLen;
+  p.rows_whole = max_row_nnz >= 0 && max_row_nnz <= p.long_row;
+  p.no_split = max_row_nnz >= 0 && max_row_nnz < (2 << p.seg_shift);
   if (p.rows_whole) p.nslots = 0;
 }
 

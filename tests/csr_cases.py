@@ -1,6 +1,19 @@
 """Synthetic CSR matrices with chosen row lengths, for the GPU parity tests
-of the long-row paths (column panels, column slices)."""
+of the long-row paths (column panels, column slices), and the library's
+documented rule for which rows it sums whole."""
 import numpy as np
+
+
+def whole_row_max(nnz):
+    """Longest row the warp-per-row family sums in one piece (in CSR order,
+    so bit-identical to the fp32 restatement) for a matrix of nnz nonzeros:
+    rows shorter than two segments.  The segment is 256 nonzeros, halved
+    (down to 32) while the matrix holds fewer than 4096 segments' worth, so
+    that a small matrix's long rows still split over the GPU."""
+    seg = 256
+    while seg > 32 and nnz // seg < 4096:
+        seg //= 2
+    return 2 * seg - 1
 
 
 def csr_from_lengths(lens, K, seed, narrow=None, unsorted_rows=()):

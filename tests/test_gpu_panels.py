@@ -8,7 +8,7 @@ row's pieces in column order.  These tests put such rows next to the cases
 that must fall back to the ordinary long-row segments (unsorted columns,
 skewed panel loads, a workspace sized without the panel tables) and check
 every row against the fp64 oracle at the 1e-5 bar, plus bitwise agreement
-with the fp32 CSR-order restatement on rows of <= 511 nonzeros.
+with the fp32 CSR-order restatement on the rows summed whole.
 """
 import numpy as np
 import pytest
@@ -16,7 +16,7 @@ import torch
 
 import oracle
 from csrspmm_amd import ALGORITHMS, capi, gen
-from csr_cases import csr_from_lengths, mixed_lengths
+from csr_cases import csr_from_lengths, mixed_lengths, whole_row_max
 
 pytestmark = pytest.mark.gpu
 
@@ -44,7 +44,7 @@ def check(algo, C, rowptr, colidx, vals, B, C0=None, alpha=1.0, beta=0.0, what="
     bad, ratio, _, _ = oracle.check(C, R, S, TOL)
     assert bad == 0, f"{algo} {what}: {bad} elements off (max ratio {ratio:.3g})"
     F = oracle.spmm_f32_seq(rowptr, colidx, vals, B, C0, alpha, beta)
-    whole = np.diff(rowptr) <= 511
+    whole = np.diff(rowptr) <= whole_row_max(int(rowptr[-1]))
     assert np.array_equal(C[whole].view(np.uint32), F[whole].view(np.uint32)), \
         f"{algo} {what}: short rows differ from the fp32 restatement"
 
@@ -133,7 +133,7 @@ def test_panels_base_workspace_runs_without_panels(algo, gpu):
     C_full = run(algo, rowptr, colidx, vals, B, gpu, workspace_bytes=full)
     check(algo, C_full, rowptr, colidx, vals, B, what="panel-size workspace")
     # rows summed whole agree bit for bit whichever way the long rows went
-    whole = np.diff(rowptr) <= 511
+    whole = np.diff(rowptr) <= whole_row_max(int(rowptr[-1]))
     assert np.array_equal(C_base[whole].view(np.uint32), C_full[whole].view(np.uint32))
 
 

@@ -4,11 +4,13 @@ against the CPU oracle on the same seeded inputs.
 Bar: |C - R| <= 1e-5 * max(|R|, S) elementwise
 against the fp64 oracle R (S = |alpha| sum |a b| + |beta c0|), CSR arrays
 byte-identical after the call.  Rows the kernels sum whole (every row for
-Naive/NaiveSmem, rows of < 512 nonzeros for the warp-per-row family) must
-also equal the oracle's fp32 CSR-order fma restatement bit for bit, since
-the kernels use the same order; longer rows are split into near-equal
-segments of 256..383 nonzeros whose partial sums are added in a fixed
-order, which is within the tolerance but not bitwise.
+Naive/NaiveSmem, rows shorter than two segments for the warp-per-row
+family: under 512 nonzeros on matrices of a million nonzeros or more,
+under 64..511 on smaller ones, csr_cases.whole_row_max) must also equal the
+oracle's fp32 CSR-order fma restatement bit for bit, since the kernels use
+the same order; longer rows are split into near-equal segments whose partial
+sums are added in a fixed order, which is within the tolerance but not
+bitwise.
 
 The full-size configs are checked on a row sample (every row for host and
 medium; 4096 random rows plus the 64 longest and some empty rows otherwise)
@@ -22,12 +24,12 @@ import torch
 
 import oracle
 from csrspmm_amd import ALGORITHMS, capi, configs, gen
+from csr_cases import whole_row_max
 from golden_cases import load, names
 
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-5
-WHOLE_MAX = 511  # longest row the warp-per-row family sums in one piece
 WHOLE_ROW_ALGOS = {"Naive", "NaiveSmem"}
 
 
@@ -64,7 +66,8 @@ def assert_parity(algo, C, rowptr, colidx, vals, B, C0, alpha, beta, rows=None, 
     F = oracle.spmm_f32_seq(rowptr, colidx, vals, B, C0, alpha, beta, c0_zero=c0_zero, rows=rows)
     ridx = np.arange(rowptr.size - 1) if rows is None else np.asarray(rows)
     lens = rowptr[ridx + 1] - rowptr[ridx]
-    whole = np.ones_like(lens, dtype=bool) if algo in WHOLE_ROW_ALGOS else lens <= WHOLE_MAX
+    whole = (np.ones_like(lens, dtype=bool) if algo in WHOLE_ROW_ALGOS
+             else lens <= whole_row_max(int(rowptr[-1])))
     a = Cs[whole].view(np.uint32)
     b = F[whole].view(np.uint32)
     # +0 and -0 only differ in sign bits; NaN payloads are not compared.

@@ -8,7 +8,7 @@ slice order (sparser rows), sharing the plan and the combine.  These
 tests cover a last partial slice, long rows on segments, the beta epilogue,
 padded leading dimensions and the scalar-column kernels, against the fp64
 oracle at the 1e-5 bar and bitwise against the fp32 CSR-order restatement on
-rows of <= 511 nonzeros.
+the rows summed whole (csr_cases.whole_row_max).
 """
 import numpy as np
 import pytest
@@ -16,7 +16,7 @@ import torch
 
 import oracle
 from csrspmm_amd import ALGORITHMS, capi, gen
-from csr_cases import csr_from_lengths, mixed_lengths
+from csr_cases import csr_from_lengths, mixed_lengths, whole_row_max
 
 pytestmark = pytest.mark.gpu
 
@@ -30,7 +30,7 @@ def check(algo, C, rowptr, colidx, vals, B, C0=None, alpha=1.0, beta=0.0, what="
     bad, ratio, _, _ = oracle.check(C, R, S, TOL)
     assert bad == 0, f"{algo} {what}: {bad} elements off (max ratio {ratio:.3g})"
     F = oracle.spmm_f32_seq(rowptr, colidx, vals, B, C0, alpha, beta)
-    whole = np.diff(rowptr) <= 511
+    whole = np.diff(rowptr) <= whole_row_max(int(rowptr[-1]))
     assert np.array_equal(C[whole].view(np.uint32), F[whole].view(np.uint32)), \
         f"{algo} {what}: short rows differ from the fp32 restatement"
 
