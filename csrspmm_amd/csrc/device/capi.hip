@@ -41,7 +41,9 @@ WorkspaceLayout workspace_layout(int M, int K, int N, int nnz, int P) {
     P = L.P;
     L.nwin = (int)(((long long)nnz + kPanelMinLen - 1) / kPanelMinLen);
     const long long per_row = (long long)P * L.ldp * (long long)sizeof(float);
-    L.nl_max = (int)std::min<long long>(L.nwin, std::max<long long>(1, kDevPanelPartialBudget / per_row));
+    L.nl_max = (int)std::min<long long>(
+        {(long long)L.nwin, std::max<long long>(1, kDevPanelPartialBudget / per_row),
+         std::max<long long>(1, ((long long)nnz + kPanelRowCapLen - 1) / kPanelRowCapLen)});
     const size_t nw = (size_t)L.nwin;
     L.win_off = off;
     off = align256(off + nw * sizeof(int4));

@@ -215,7 +215,16 @@ inline int slice_blocks_per_cu(int K, int sw, bool slice_launch) {
 // a row of len >= kPanelMinLen contains the start of window
 // id(r) = ceil(rowptr[r] / kPanelMinLen), which no other such row does, so
 // id(r) names the row in the per-window tables below.
-constexpr long long kDevPanelPartialBudget = 256LL << 20;  // bytes of piece partials, at most
+#ifndef CSRSPMM_PANEL_PARTIAL_MB
+#define CSRSPMM_PANEL_PARTIAL_MB 256
+#endif
+constexpr long long kDevPanelPartialBudget = (long long)CSRSPMM_PANEL_PARTIAL_MB << 20;  // bytes of piece partials, at most
+// A call panelizes at most nnz / kPanelRowCapLen rows as well (a quarter of
+// the nnz / kPanelMinLen possible): the main launch sizes its pieces grid for
+// nl_max rows, since the host cannot know how many there are, and a grid for
+// 8192 rows where XL has 1501 left ~25,000 blocks that exit at once, 10 us
+// of dispatch.  Rows beyond the cap, in row order, stay on segments.
+constexpr long long kPanelRowCapLen = 4LL * kPanelMinLen;
 constexpr int kDevPanelSample = 64;  // rows sampled for the panel loads
 struct DevPanels {
   int P;           // panels, ceil(K / 2^wshift) <= panel_count(K, N); 0 = off

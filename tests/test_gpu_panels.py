@@ -77,6 +77,25 @@ def test_panels_mixed_rows(algo, N, gpu):
 
 
 @pytest.mark.parametrize("algo", PANEL_ALGOS)
+def test_panels_more_rows_than_the_cap(algo, gpu):
+    # 400 rows of 1024..1299 nonzeros: more than the nnz / 4096 rows a call
+    # panelizes, so the first ones (in row order) take pieces and the rest
+    # segments, in the same call
+    K, N = 32768, 128
+    rng = np.random.default_rng(61)
+    lens = rng.integers(0, 20, size=2400)
+    lens[rng.choice(lens.size, 400, replace=False)] = rng.integers(1024, 1300, size=400)
+    rowptr, colidx, vals = csr_from_lengths(lens, K, seed=61)
+    assert np.count_nonzero(lens >= 1024) > -(-colidx.size // 4096)
+    B = gen.dense(61, gen.TAG_B, K, N)
+    print(f"[panels] cap {algo} M={lens.size} nnz={colidx.size}", flush=True)
+    C = run(algo, rowptr, colidx, vals, B, gpu)
+    check(algo, C, rowptr, colidx, vals, B, what="rows beyond the panel cap")
+    C2 = run(algo, rowptr, colidx, vals, B, gpu)
+    assert np.array_equal(C.view(np.uint32), C2.view(np.uint32))
+
+
+@pytest.mark.parametrize("algo", PANEL_ALGOS)
 def test_panels_epilogue_and_strided_b(algo, gpu):
     K, N = 65536, 128
     lens = mixed_lengths(21, M=1500)
