@@ -17,15 +17,20 @@
 // per-wave LDS stage in the Smem variants.  U independent B-row gathers are
 // issued before their fmas, keeping U x VEC x 4 bytes per lane in flight.
 //
-// Load balance (large problems, "plan" mode, three launches):
-//  * plan_kernel, one thread per row, no atomics: merge-block starts and
-//    the segment slots of long rows.
-//  * rowgroup_kernel: the first blocks take the long-row segments (partial
-//    sums to the workspace); the other blocks each take one merge block of
-//    consecutive short rows and stream their contiguous nonzeros, so
-//    gathers stay in flight across row boundaries and a row's accumulator
-//    is flushed (epilogue + store) when the stream passes its end.
-//  * combine_kernel: adds each long row's partials in a fixed order.
+// Load balance (large problems, "plan" mode):
+//  * plan_kernel, one thread per row, no atomics: merge-block starts, the
+//    segment slots of long rows and, with column panels, the window table.
+//  * with column panels, panel_window_kernel and panel_sched_kernel
+//    (panels.hip) build this call's panel schedule.
+//  * rowgroup_kernel: the first blocks take the panel pieces (when there
+//    are panels), then the long-row segments (partial sums to the
+//    workspace); the other blocks each take one merge block of consecutive
+//    short rows and stream their contiguous nonzeros, so gathers stay in
+//    flight across row boundaries and a row's accumulator is flushed
+//    (epilogue + store) when the stream passes its end.  With column slices
+//    the segment and merge blocks repeat per slice of columns.
+//  * combine_kernel: adds each split or panelized row's partials in a
+//    fixed order.
 // Everything is deterministic (no float atomics): results repeat bit for bit.
 
 #include "common.hpp"
