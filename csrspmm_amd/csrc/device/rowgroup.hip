@@ -560,17 +560,39 @@ __device__ __forceinline__ f4 sum_strided(const float* src, const int* pieces, i
   return acc;
 }
 
-// Sum over the 64 / GC lane groups of a wave by a fixed xor-shuffle tree;
-// every group ends with the total.
+// The value of lane (this lane ^ OFF), OFF in {8, 16, 32}: a DPP row_ror:8
+// (rotating a 16-lane row by half of it is the xor), a ds_swizzle swapping the
+// 16-lane halves of each 32-lane group (bit mode: and 0x1f, xor 0x10), and a
+// ds_bpermute across the 32-lane halves, which no gfx9 DPP or swizzle crosses.
+template <int OFF>
+__device__ __forceinline__ float lane_xor(float v) {
+  const int x = __builtin_bit_cast(int, v);
+  int y;
+  if constexpr (OFF == 8) {
+    y = __builtin_amdgcn_update_dpp(0, x, 0x128 /* row_ror:8 */, 0xF, 0xF, false);
+  } else if constexpr (OFF == 16) {
+    y = __builtin_amdgcn_ds_swizzle(x, 0x401F);
+  } else {
+    static_assert(OFF == 32, "lane_xor: offsets 8, 16, 32");
+    y = __builtin_amdgcn_ds_bpermute((lane_id() ^ 32) << 2, x);
+  }
+  return __builtin_bit_cast(float, y);
+}
+
+template <int OFF>
+__device__ __forceinline__ f4 add_lane_xor(f4 v) {
+  return f4{v.x + lane_xor<OFF>(v.x), v.y + lane_xor<OFF>(v.y), v.z + lane_xor<OFF>(v.z),
+            v.w + lane_xor<OFF>(v.w)};
+}
+
+// Sum over the 64 / GC lane groups of a wave by a fixed xor tree (offsets GC,
+// 2 GC, ... 32); every group ends with the total.  All lanes take part.
 template <int GC>
 __device__ __forceinline__ f4 wave_group_sum(f4 v) {
-#pragma unroll
-  for (int off = GC; off < 64; off <<= 1) {
-    v.x += __shfl_xor(v.x, off);
-    v.y += __shfl_xor(v.y, off);
-    v.z += __shfl_xor(v.z, off);
-    v.w += __shfl_xor(v.w, off);
-  }
+  static_assert(GC == 8 || GC == 16 || GC == 32 || GC == 64, "group widths of the combine");
+  if constexpr (GC <= 8) v = add_lane_xor<8>(v);
+  if constexpr (GC <= 16) v = add_lane_xor<16>(v);
+  if constexpr (GC <= 32) v = add_lane_xor<32>(v);
   return v;
 }
 
