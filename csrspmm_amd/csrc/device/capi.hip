@@ -47,6 +47,8 @@ WorkspaceLayout workspace_layout(int M, int K, int N, int nnz, int P) {
     const size_t nw = (size_t)L.nwin;
     L.win_off = off;
     off = align256(off + nw * sizeof(int4));
+    L.flag_off = off;
+    off = align256(off + nw);
     L.pidx_off = off;
     off = align256(off + nw * sizeof(int));
     L.list_off = off;
@@ -54,7 +56,7 @@ WorkspaceLayout workspace_layout(int M, int K, int N, int nnz, int P) {
     L.bnd_off = off;
     off = align256(off + nw * ((size_t)P + 1) * sizeof(int));
     L.sched_off = off;
-    off = align256(off + (size_t)(kXcds + 2) * sizeof(int));
+    off = align256(off + (size_t)(kPanelHist + P) * sizeof(int));
     L.part_off = off;
     off = align256(off + (size_t)L.nl_max * (size_t)P * (size_t)L.ldp * sizeof(float));
   }
@@ -73,6 +75,7 @@ void bind_workspace(Problem& p, void* ws, const WorkspaceLayout& L, int mblk) {
   p.nblocks = merge_blocks(p.M, p.nnz, mblk);
 
   p.dp = DevPanels{};
+  p.dp_flag = nullptr;
   if (L.P > 0) {
     p.dp.P = L.P;
     p.dp.wshift = L.wshift;
@@ -84,6 +87,7 @@ void bind_workspace(Problem& p, void* ws, const WorkspaceLayout& L, int mblk) {
     p.dp.bnd = reinterpret_cast<int*>(b + L.bnd_off);
     p.dp.sched = reinterpret_cast<int*>(b + L.sched_off);
     p.dp.part = reinterpret_cast<float*>(b + L.part_off);
+    p.dp_flag = reinterpret_cast<unsigned char*>(b + L.flag_off);
   }
 }
 

@@ -470,8 +470,11 @@ __device__ __forceinline__ void plan_row_entries(const Problem& p, int r, int b_
   for (int s = s0 + first; s < s1; s += step)
     p.seg_info[s] = (s - s0) < nseg ? make_int2(r, s - s0) : make_int2(-1, 0);
   // the first window of a long row is the row's id
-  for (int w = w0 + first; w < w1; w += step)
-    p.dp.win[w] = make_int4(r, x0, x1, (w == w0 && x1 - x0 >= kPanelMinLen) ? 1 : 0);
+  for (int w = w0 + first; w < w1; w += step) {
+    const int id = (w == w0 && x1 - x0 >= kPanelMinLen) ? 1 : 0;
+    p.dp.win[w] = make_int4(r, x0, x1, id);
+    p.dp_flag[w] = (unsigned char)id;
+  }
 }
 
 // A row with more table entries than this has them written by its whole
@@ -487,11 +490,14 @@ constexpr int kPlanSoloEntries = CSRSPMM_PLAN_SOLO_ENTRIES;
 // One thread per row r in [0, M]: the merge-block starts that fall on r, the
 // segment slots r owns and, with column panels, the windows that begin in r.
 // Every entry the main kernel reads is written here on each call, from
-// rowptr alone (no counters to reset, no atomics).
+// rowptr alone (no atomics); with panels, block 0 also zeroes the sampled
+// panel loads that panel_window_kernel adds to.
 __global__ __launch_bounds__(256) void plan_kernel(Problem p) {
   const int stride = gridDim.x * blockDim.x;
   const int mshift = __builtin_ctz((unsigned)p.mblk);  // mblk is a power of two
   const int lane = lane_id();
+  if (p.dp.P > 0 && blockIdx.x == 0)
+    for (int q = (int)threadIdx.x; q < p.dp.P; q += blockDim.x) p.dp.sched[kPanelHist + q] = 0;
   // block-uniform trip count, so every wave reaches the ballot below whole
   for (int base = blockIdx.x * blockDim.x; base <= p.M; base += stride) {
     const int r = base + (int)threadIdx.x;

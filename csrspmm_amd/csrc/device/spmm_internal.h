@@ -226,19 +226,20 @@ constexpr long long kDevPanelPartialBudget = (long long)CSRSPMM_PANEL_PARTIAL_MB
 // of dispatch.  Rows beyond the cap, in row order, stay on segments.
 constexpr long long kPanelRowCapLen = 4LL * kPanelMinLen;
 constexpr int kDevPanelSample = 64;  // rows sampled for the panel loads
+constexpr int kPanelHist = kXcds + 2;
 struct DevPanels {
   int P;           // panels, ceil(K / 2^wshift) <= panel_count(K, N); 0 = off
   int wshift;      // columns per panel = 2^wshift: ceil(K / panel_count) rounded up to a power
                    // of two, so a column's panel is a shift
   int nwin;        // windows, ceil(nnz / kPanelMinLen)
   int nl_max;      // panelized rows at most (rows of the partial buffer)
-  int4* win;       // [nwin] (r, rowptr[r], rowptr[r+1], flag) for the row r holding position
-                   // w * kPanelMinLen; flag 1: w = id(r) of a long row whose columns are
-                   // sorted and in range
+  int4* win;       // [nwin] (r, rowptr[r], rowptr[r+1], w == id(r) of a long row) for the
+                   // row r holding position w * kPanelMinLen
   int* pidx;       // [nwin] compact index of the panelized row with id w, else -1
   int* list;       // [nl_max] ids of the panelized rows, in row order
   int* bnd;        // [nwin][P + 1] absolute position where panel q starts in the row with id w
-  int* sched;      // [0] = nl (0: no row panelized this call), [1 .. kXcds + 1] = XCD panel ranges
+  int* sched;      // [0] = nl (0: no row panelized this call), [1 .. kXcds + 1] = XCD panel
+                   // ranges, [kPanelHist + q] = sampled nonzeros in panel q
   float* part;     // [nl_max][P][ldp] piece partial sums
 };
 
@@ -302,6 +303,11 @@ struct Problem {
   // them above shifted the kernel-argument offsets of the fields after them
   // and, with the same kernel code, measured 4-5% slower on the XL configs.
   int seg_shift, slot_shift, long_row;
+  // A per-call panel table added after the fields above, for the same
+  // reason: dp_flag[w] = 1 when window w is id(r) of a long row whose columns
+  // are sorted and in range (plan_kernel sets it from rowptr,
+  // panel_window_kernel clears it), else 0.
+  unsigned char* dp_flag;
 };
 
 // Segments of a row of len nonzeros under the problem's geometry and hint.
@@ -321,7 +327,7 @@ inline void set_row_hint(Problem& p, int max_row_nnz) {
 // the per-call panel tables and partial buffer after the base sections.
 struct WorkspaceLayout {
   size_t block_start_off, seg_info_off, partials_off, base_total;
-  size_t win_off, pidx_off, list_off, bnd_off, sched_off, part_off, total;
+  size_t win_off, flag_off, pidx_off, list_off, bnd_off, sched_off, part_off, total;
   int nslots, nblocks;
   long long ldp;
   int P, wshift, nwin, nl_max;
@@ -351,9 +357,9 @@ hipError_t launch_naive_smem(const Problem& p, hipStream_t s);
 // vec = 1 (scalar columns) or 4 (float4 columns); lds = stage (col,val) in LDS.
 hipError_t launch_rowgroup(const Problem& p, int vec, bool lds, hipStream_t s);
 
-// Per-call panel schedule (panels.hip): after plan_kernel has filled
-// dp.win_row / dp.flag, find the panel boundaries of the long rows, then
-// compact the panelized rows and deal the panels to the XCDs.
+// Per-call panel schedule (panels.hip): after plan_kernel has filled dp.win
+// and dp_flag, find the panel boundaries of the long rows, then compact the
+// panelized rows and deal the panels to the XCDs.
 hipError_t launch_panel_schedule(const Problem& p, hipStream_t s);
 
 // Benchmark timing hook: no-ops unless csrspmm_timing_enable(1) was called.
