@@ -30,6 +30,8 @@ HIP_API = {
     "csrspmm_resolve_algorithm": (_c_int, [_c_int, _c_int]),
     "csrspmm_workspace_bytes": (_c_size_t, [_c_int, _c_int, _c_int, _c_int]),
     "csrspmm_workspace_bytes_ex": (_c_size_t, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
+    "csrspmm_workspace_panel_info": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                              ctypes.POINTER(_c_ll)]),
     "csrspmm_spmm_f32": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p, _c_void_p,
                                   _c_void_p, _c_int, _c_void_p, _c_ll, _c_void_p, _c_ll, _c_float,
                                   _c_float, _c_void_p]),
@@ -164,6 +166,25 @@ def spmm(algo, rowptr, colidx, vals, B, C, alpha, beta, *, M=None, K=None, hint=
                                      _ptr(workspace), wsz, ctypes.c_void_p(stream))
     check(st, f"csrspmm_spmm {algo}")
     return C
+
+
+def panelized_rows(algo, rowptr, colidx, vals, B, C, alpha=1.0, beta=0.0, *, hint=-1):
+    """Runs one per-call product (as spmm, with a workspace of
+    csrspmm_workspace_bytes_ex bytes) and returns how many rows it cut into
+    column panels: None when a call of this shape uses no panels, 0 when the
+    panel loads were too skewed.  Synchronizes the device."""
+    a = ALGO[algo] if isinstance(algo, str) else int(algo)
+    M, K, N, nnz = rowptr.numel() - 1, B.shape[0], C.shape[1], vals.numel()
+    lib = hip()
+    off = ctypes.c_longlong(-1)
+    P = lib.csrspmm_workspace_panel_info(a, M, K, N, nnz, hint, ctypes.byref(off))
+    need = lib.csrspmm_workspace_bytes_ex(a, M, K, N, nnz, hint)
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device=C.device)
+    spmm(algo, rowptr, colidx, vals, B, C, alpha, beta, hint=hint, workspace=ws)
+    torch.cuda.synchronize(C.device)
+    if P <= 0:
+        return None
+    return int(ws[off.value:off.value + 4].view(torch.int32).item())
 
 
 class Plan:

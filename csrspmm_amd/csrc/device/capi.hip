@@ -408,15 +408,30 @@ size_t csrspmm_workspace_bytes(int algo, int M, int N, int nnz) {
   return workspace_layout(M, 0, N, nnz, 0).base_total;
 }
 
-size_t csrspmm_workspace_bytes_ex(int algo, int M, int K, int N, int nnz, int max_row_nnz_hint) {
+// The panels of a per-call product as far as the shape tells (pointer
+// alignment is checked per call); -1 when the call makes no plan.
+static int shape_panels(int algo, int M, int K, int N, int nnz, int hint) {
   algo = resolve_algorithm(algo, N);
-  if (M <= 0 || N <= 0 || nnz < 0 || K < 0 || !wants_plan(algo, M, nnz, max_row_nnz_hint)) return 0;
-  // float4 columns as far as the shape tells (pointer alignment is checked per call)
+  if (M <= 0 || N <= 0 || nnz < 0 || K < 0 || !wants_plan(algo, M, nnz, hint)) return -1;
   const bool fp4 = (algo == CSRSPMM_ALGO_WARP_PER_ROW_FP4 || algo == CSRSPMM_ALGO_WARP_PER_ROW_SMEM_FP4) &&
                    N % 4 == 0;
-  int P = per_call_panels(fp4 ? 4 : 1, true, K, N, nnz, max_row_nnz_hint);
+  int P = per_call_panels(fp4 ? 4 : 1, true, K, N, nnz, hint);
   if (slice_width(K, N, P > 0) > 0) P = 0;
-  return workspace_layout(M, K, N, nnz, P).total;
+  return P;
+}
+
+size_t csrspmm_workspace_bytes_ex(int algo, int M, int K, int N, int nnz, int max_row_nnz_hint) {
+  const int P = shape_panels(algo, M, K, N, nnz, max_row_nnz_hint);
+  return P < 0 ? 0 : workspace_layout(M, K, N, nnz, P).total;
+}
+
+int csrspmm_workspace_panel_info(int algo, int M, int K, int N, int nnz, int max_row_nnz_hint,
+                                 long long* nl_offset) {
+  const int P = shape_panels(algo, M, K, N, nnz, max_row_nnz_hint);
+  if (P <= 0) return 0;
+  const WorkspaceLayout L = workspace_layout(M, K, N, nnz, P);
+  if (nl_offset) *nl_offset = (long long)L.sched_off;  // sched[0] = nl
+  return L.P;
 }
 
 int csrspmm_spmm_f32(int algo, int M, int K, int N, int nnz, const int* rowptr, const int* colidx,

@@ -92,6 +92,16 @@ size_t csrspmm_workspace_bytes(int algo, int M, int N, int nnz);
  * csrspmm_workspace_bytes but less than this size runs without panels. */
 size_t csrspmm_workspace_bytes_ex(int algo, int M, int K, int N, int nnz, int max_row_nnz_hint);
 
+/* Where a per-call workspace of csrspmm_workspace_bytes_ex bytes holds the
+ * call's column-panel decision, for tests and tuning: returns the number of
+ * column panels such a call uses (0: none, and *nl_offset is left alone)
+ * when B and C rows are 16-byte aligned, and sets *nl_offset to the byte
+ * offset of an int32 that the call writes: the number of rows it panelized,
+ * 0 when the panel loads were too skewed.  Reading it needs the call to have
+ * finished.  No counterpart in the reference, which has no panels. */
+int csrspmm_workspace_panel_info(int algo, int M, int K, int N, int nnz, int max_row_nnz_hint,
+                                 long long* nl_offset);
+
 /*
  * The SpMM.  Replaces csrspmm::spmm's dispatch to launch_<variant>
  * (reference src/csrspmm.cpp:28-71, src/host/spmm_launcher.cu:11-171) and the

@@ -82,3 +82,24 @@ def test_column_checksums(cfg_name, gpu):
     err = np.abs(got - want)
     assert (err <= TOL * bound).all(), \
         f"{cfg_name}: column sums off, worst {np.max(err / bound):.3g} of the 1e-5 bound"
+
+
+@pytest.mark.parametrize("cfg_name,algo,expect", [
+    ("xl", "Auto", "long"), ("xl98", "Auto", "long"), ("rmat", "WarpPerRowFp4", "skewed")])
+def test_panel_decision(cfg_name, algo, expect, gpu):
+    """The per-call schedule's decision on the bench configs: the power-law
+    configs (columns uniform) panelize every row of >= 1024 nonzeros, all
+    under the nnz / 4096 cap; R-MAT's hot columns read as skewed."""
+    cfg = configs.CONFIGS[cfg_name]
+    a = cfg.csr()
+    print(f"[fullsize] panel decision {cfg_name} {algo}", flush=True)
+    C = torch.empty((a.M, cfg.N), device=gpu)
+    nl = capi.panelized_rows(algo, dev_t(a.rowptr, gpu), dev_t(a.colidx, gpu), dev_t(a.vals, gpu),
+                             dev_t(cfg.B(a.K), gpu), C)
+    long_rows = int(np.count_nonzero(np.diff(a.rowptr) >= 1024))
+    if expect == "long":
+        assert long_rows <= -(-a.nnz // 4096)
+        assert nl == long_rows
+    else:
+        assert nl == 0
+

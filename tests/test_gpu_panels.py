@@ -49,6 +49,15 @@ def check(algo, C, rowptr, colidx, vals, B, C0=None, alpha=1.0, beta=0.0, what="
         f"{algo} {what}: short rows differ from the fp32 restatement"
 
 
+def run_nl(algo, rowptr, colidx, vals, B, dev):
+    """(C, rows the call panelized, None without panels)."""
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)  # noqa: E731
+    M, N = rowptr.size - 1, B.shape[1]
+    dC = torch.full((M, N), float("nan"), device=dev)
+    nl = capi.panelized_rows(algo, t(rowptr), t(colidx), t(vals), t(B), dC)
+    return dC.cpu().numpy(), nl
+
+
 def panel_bytes(algo, M, K, N, nnz):
     lib = capi.hip()
     a = capi.ALGO[algo]
@@ -72,8 +81,12 @@ def test_panels_mixed_rows(algo, N, gpu):
     C = run(algo, rowptr, colidx, vals, B, gpu)
     check(algo, C, rowptr, colidx, vals, B, what=f"mixed N={N}")
     # repeated calls are bit-identical (no atomics in the float path)
-    C2 = run(algo, rowptr, colidx, vals, B, gpu)
+    C2, nl = run_nl(algo, rowptr, colidx, vals, B, gpu)
     assert np.array_equal(C.view(np.uint32), C2.view(np.uint32))
+    if full > base:
+        # columns uniform apart from one row: every row of >= 1024 nonzeros
+        # (sorted, fewer than the nnz / 4096 cap) is panelized
+        assert nl == np.count_nonzero(lens >= 1024)
 
 
 @pytest.mark.parametrize("algo", PANEL_ALGOS)
@@ -91,8 +104,9 @@ def test_panels_more_rows_than_the_cap(algo, gpu):
     print(f"[panels] cap {algo} M={lens.size} nnz={colidx.size}", flush=True)
     C = run(algo, rowptr, colidx, vals, B, gpu)
     check(algo, C, rowptr, colidx, vals, B, what="rows beyond the panel cap")
-    C2 = run(algo, rowptr, colidx, vals, B, gpu)
+    C2, nl = run_nl(algo, rowptr, colidx, vals, B, gpu)
     assert np.array_equal(C.view(np.uint32), C2.view(np.uint32))
+    assert nl == -(-colidx.size // 4096), "the first nnz / 4096 long rows are panelized"
 
 
 @pytest.mark.parametrize("algo", PANEL_ALGOS)
@@ -120,8 +134,9 @@ def test_panels_unsorted_row_falls_back(algo, gpu):
     r_uns = int(np.nonzero(lens == 5000)[0][0])
     rowptr, colidx, vals = csr_from_lengths(lens, K, seed=33, unsorted_rows={r_uns})
     B = gen.dense(13, gen.TAG_B, K, N)
-    C = run(algo, rowptr, colidx, vals, B, gpu)
+    C, nl = run_nl(algo, rowptr, colidx, vals, B, gpu)
     check(algo, C, rowptr, colidx, vals, B, what="one unsorted long row")
+    assert nl == np.count_nonzero(lens >= 1024) - 1, "all long rows but the unsorted one"
 
 
 @pytest.mark.parametrize("algo", PANEL_ALGOS)
@@ -135,8 +150,9 @@ def test_panels_skewed_loads_fall_back(algo, gpu):
     narrow = {r: (0, 4096) for r in np.nonzero(lens >= 2048)[0].tolist()}
     rowptr, colidx, vals = csr_from_lengths(lens, K, seed=44, narrow=narrow)
     B = gen.dense(14, gen.TAG_B, K, N)
-    C = run(algo, rowptr, colidx, vals, B, gpu)
+    C, nl = run_nl(algo, rowptr, colidx, vals, B, gpu)
     check(algo, C, rowptr, colidx, vals, B, what="skewed panel loads")
+    assert nl == 0, "skewed panel loads keep every row on segments"
 
 
 @pytest.mark.parametrize("algo", PANEL_ALGOS)
