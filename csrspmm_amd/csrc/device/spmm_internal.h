@@ -185,10 +185,13 @@ inline bool slice_launches(int M, int nnz) {
 }
 // 0 (no slices) or the slice width for a K x N B; `panels` tells that the
 // per-call column panels could apply (they are kept, unsliced, for N <= 128).
+#ifndef CSRSPMM_SLICE_MIN_MB
+#define CSRSPMM_SLICE_MIN_MB 32
+#endif
 inline int slice_width(int K, int N, bool panels) {
   const long long full = (long long)K * N * 4;
   const long long band = (long long)K * kSliceWidth * 4;
-  if (N < 2 * kSliceWidth || full < (32LL << 20)) return 0;
+  if (N < 2 * kSliceWidth || full < ((long long)CSRSPMM_SLICE_MIN_MB << 20)) return 0;
   if (N <= 128 && panels) return 0;
   if (band > (16LL << 20) && full < (1LL << 30)) return 0;
   return kSliceWidth;
