@@ -92,7 +92,7 @@ void bind_workspace(Problem& p, void* ws, const WorkspaceLayout& L, int mblk) {
 }
 
 int per_call_panels(int vec, bool plan, int K, int N, int nnz, int hint) {
-  if (vec != 4 || !plan || nnz < kPanelMinLen) return 0;
+  if ((vec != 4 && N < kPanelMinScalarN) || !plan || nnz < kPanelMinLen) return 0;
   if (hint >= 0 && hint < kPanelMinLen) return 0;
   return panel_count(K, N);
 }

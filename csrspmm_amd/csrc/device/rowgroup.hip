@@ -441,7 +441,10 @@ __global__ __launch_bounds__(kWaves * 64) void rowgroup_kernel(Problem p, int pi
   __shared__ int2 stage_all[LDS ? kWaves * 64 : 1];
   int2* stage = stage_all + (LDS ? wave * 64 : 0);
 
-  if constexpr (VEC == 4) {  // column panels are built for float4 columns only
+  // Column panels reach the float4 kernels and the scalar ones of N > 64
+  // (per_call_panels); the scalar N <= 64 kernel is compiled without the
+  // pieces, which cost it 9% on R-MAT as dead code.
+  if constexpr (VEC == 4 || T >= 2) {
     if ((int)blockIdx.x < piece_blocks) {
       pieces_body<VEC, G, T, U, LDS>(p, (int)blockIdx.x, gl, gbase, gid, stage);
       return;
@@ -738,7 +741,7 @@ hipError_t launch_rg(const Problem& p, hipStream_t s) {
   const int seg_blocks =
       (p.plan && p.nslots > 0) ? std::min(kSegBlocksMax, div_up_host(p.nslots, GPB)) : 0;
   int piece_blocks = 0;
-  if (VEC == 4 && p.dp.P > 0) {
+  if ((VEC == 4 || T >= 2) && p.dp.P > 0) {
     // chunks of the longest XCD list possible: ceil(P / kXcds) panels x nl_max rows
     const long long per_xcd = (long long)div_up_host(p.dp.P, kXcds) * p.dp.nl_max;
     const long long chunks = (per_xcd + (long long)kPiecesPerGroup * GPB - 1) / ((long long)kPiecesPerGroup * GPB);

@@ -138,7 +138,8 @@ constexpr long long kPlanMinItems = 1 << 16;
 constexpr int kXcds = 8;
 
 // Column panels.  A row of at least kPanelMinLen nonzeros with sorted
-// columns, on a B of at least 16 MiB with N <= 256 and float4 columns, is cut
+// columns, on a B of at least 16 MiB with N <= 256 (float4 columns, or scalar
+// ones from N = 128), is cut
 // at the boundaries of P column panels (P a power of two, kXcds..256, so that
 // a panel's band of B is about kPanelBandBytes).  Each XCD walks its own
 // panels in column order, so the band it gathers from stays in its L2.  Stored
@@ -156,6 +157,10 @@ constexpr int kXcds = 8;
 constexpr int kPanelMinLen = CSRSPMM_PANEL_MIN_LEN;
 constexpr long long kPanelBandBytes = (long long)CSRSPMM_PANEL_BAND_KB * 1024;
 constexpr int kPanelMaxPanels = 256;
+// Scalar-column (VEC = 1) calls use panels from N = 128 up.  Measured on
+// MI355X, WarpPerRowSmem on XL: N = 128 648 -> 451 us, N = 256 1252 -> 831;
+// at N = 64 the pieces lost (331 -> 350 us), and the float4 form leads there.
+constexpr int kPanelMinScalarN = 128;
 constexpr int kPanelSkewMax = 4;  // panels stay off when max panel load > 4 x mean
 static_assert(kPanelMinLen > kLongRow, "panelized rows are long rows");
 
@@ -337,8 +342,9 @@ struct WorkspaceLayout {
 };
 WorkspaceLayout workspace_layout(int M, int K, int N, int nnz, int P);
 
-// Panels the per-call path uses for this problem (0: none): float4 columns,
-// the plan on, and a row of kPanelMinLen nonzeros possible under the hint.
+// Panels the per-call path uses for this problem (0: none): float4 columns
+// (or scalar ones from N = kPanelMinScalarN), the plan on, and a row of
+// kPanelMinLen nonzeros possible under the hint.
 int per_call_panels(int vec, bool plan, int K, int N, int nnz, int hint);
 
 // Bind the plan pointers of p into a workspace base pointer; merge blocks of

@@ -147,8 +147,9 @@ def test_csr_tools_argument_errors_without_device():
 
 
 def test_workspace_bytes_ex_panels():
-    """The panel tables are reserved only for float4 variants on a B of
-    >= 16 MiB when a row of >= 1024 nonzeros is possible under the hint."""
+    """The panel tables are reserved on a B of >= 16 MiB with N <= 256 (for
+    scalar columns from N = 128) when a row of >= 1024 nonzeros is possible
+    under the hint."""
     lib = capi.hip()
     a = capi.ALGO["WarpPerRowSmemFp4"]
     M, K, N, nnz = 262144, 262144, 128, 8453223
@@ -160,7 +161,9 @@ def test_workspace_bytes_ex_panels():
     # partials at most 256 MiB, plus tables of a few MiB
     assert full - base <= (256 << 20) + (8 << 20)
     s = capi.ALGO["WarpPerRowSmem"]
-    assert lib.csrspmm_workspace_bytes_ex(s, M, K, N, nnz, -1) == lib.csrspmm_workspace_bytes(s, M, N, nnz)
+    assert lib.csrspmm_workspace_bytes_ex(s, M, K, N, nnz, -1) > lib.csrspmm_workspace_bytes(s, M, N, nnz)
+    assert lib.csrspmm_workspace_bytes_ex(s, M, K, 64, nnz, -1) == lib.csrspmm_workspace_bytes(s, M, 64, nnz)
+    assert lib.csrspmm_workspace_bytes_ex(a, M, K, 64, nnz, -1) > lib.csrspmm_workspace_bytes(a, M, 64, nnz)
     assert lib.csrspmm_workspace_bytes_ex(a, M, 1024, N, nnz, -1) == base  # B of 512 KiB
     assert lib.csrspmm_workspace_bytes_ex(a, M, K, 512, nnz, -1) == lib.csrspmm_workspace_bytes(a, M, 512, nnz)
     assert lib.csrspmm_workspace_bytes_ex(capi.ALGO["Naive"], M, K, N, nnz, -1) == 0

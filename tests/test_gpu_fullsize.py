@@ -85,7 +85,8 @@ def test_column_checksums(cfg_name, gpu):
 
 
 @pytest.mark.parametrize("cfg_name,algo,expect", [
-    ("xl", "Auto", "long"), ("xl98", "Auto", "long"), ("rmat", "WarpPerRowFp4", "skewed")])
+    ("xl", "Auto", "long"), ("xl", "WarpPerRowSmem", "long"), ("xl98", "Auto", "long"),
+    ("rmat", "WarpPerRowFp4", "skewed")])
 def test_panel_decision(cfg_name, algo, expect, gpu):
     """The per-call schedule's decision on the bench configs: the power-law
     configs (columns uniform) panelize every row of >= 1024 nonzeros, all

@@ -1,7 +1,8 @@
 """GPU parity of the per-call column panels.
 
-With float4 columns (WarpPerRowFp4 / WarpPerRowSmemFp4 / Auto at N >= 128),
-a B of at least 16 MiB and N <= 256, every SpMM call cuts rows of >= 1024
+With float4 columns (WarpPerRowFp4 / WarpPerRowSmemFp4), or scalar ones
+from N = 128 (WarpPerRow / WarpPerRowSmem, Auto), a B of at least 16 MiB and
+N <= 256, every SpMM call cuts rows of >= 1024
 nonzeros with sorted columns at column-panel boundaries on the device, sums
 the pieces panel by panel (each XCD walking its own panels) and adds a
 row's pieces in column order.  These tests put such rows next to the cases
@@ -21,7 +22,15 @@ from csr_cases import csr_from_lengths, mixed_lengths, whole_row_max
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-5
-PANEL_ALGOS = ["WarpPerRowFp4", "WarpPerRowSmemFp4", "Auto"]
+PANEL_ALGOS = ["WarpPerRowFp4", "WarpPerRowSmemFp4", "Auto", "WarpPerRow", "WarpPerRowSmem"]
+
+
+def expects_panels(algo, N):
+    """Whether a per-call product on a 16 MiB+ B with N <= 256 takes panels:
+    float4 columns at any N, scalar columns (Auto below N = 128 included) from
+    N = 128."""
+    return algo in ("WarpPerRowFp4", "WarpPerRowSmemFp4") or (
+        algo in ("WarpPerRow", "WarpPerRowSmem", "Auto") and N >= 128)
 
 
 def run(algo, rowptr, colidx, vals, B, dev, C0=None, alpha=1.0, beta=0.0, workspace_bytes=None):
@@ -76,8 +85,10 @@ def test_panels_mixed_rows(algo, N, gpu):
     B = gen.dense(11, gen.TAG_B, K, N)
     print(f"[panels] mixed {algo} N={N} M={lens.size} nnz={colidx.size}", flush=True)
     base, full = panel_bytes(algo, lens.size, K, N, colidx.size)
-    if algo in ("WarpPerRowFp4", "WarpPerRowSmemFp4") or (algo == "Auto" and N >= 128):
-        assert full > base, "float4 variants on a 16 MiB B reserve the panel tables"
+    if expects_panels(algo, N):
+        assert full > base, "a 16 MiB B reserves the panel tables"
+    else:
+        assert full == base
     C = run(algo, rowptr, colidx, vals, B, gpu)
     check(algo, C, rowptr, colidx, vals, B, what=f"mixed N={N}")
     # repeated calls are bit-identical (no atomics in the float path)
@@ -184,7 +195,7 @@ def test_panels_odd_k(algo, K, gpu):
     rowptr, colidx, vals = csr_from_lengths(lens, K, seed=K)
     B = gen.dense(16, gen.TAG_B, K, N)
     base, full = panel_bytes(algo, lens.size, K, N, colidx.size)
-    if algo != "Auto" or N >= 128:
+    if expects_panels(algo, N):
         assert full > base
     C = run(algo, rowptr, colidx, vals, B, gpu)
     check(algo, C, rowptr, colidx, vals, B, what=f"K={K}")
