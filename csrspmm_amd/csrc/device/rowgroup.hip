@@ -427,7 +427,11 @@ __device__ __forceinline__ void rowgroup_block(const Problem& p, int bid, int se
   }
 }
 
-template <int VEC, int G, int T, int U, bool LDS>
+// PIECES: compiled with the panel pieces (launched only for calls with
+// column panels).  The kernels of calls without them are compiled without
+// that code, which as dead code cost the scalar N <= 64 kernel 9% on R-MAT
+// and the scalar N = 128 / 256 kernels 3-18% on the reference's sweep shapes.
+template <int VEC, int G, int T, int U, bool LDS, bool PIECES>
 __global__ __launch_bounds__(kWaves * 64) void rowgroup_kernel(Problem p, int piece_blocks,
                                                                 int seg_blocks, int slice_blocks,
                                                                 int slice0) {
@@ -441,10 +445,7 @@ __global__ __launch_bounds__(kWaves * 64) void rowgroup_kernel(Problem p, int pi
   __shared__ int2 stage_all[LDS ? kWaves * 64 : 1];
   int2* stage = stage_all + (LDS ? wave * 64 : 0);
 
-  // Column panels reach the float4 kernels and the scalar ones of N > 64
-  // (per_call_panels); the scalar N <= 64 kernel is compiled without the
-  // pieces, which cost it 9% on R-MAT as dead code.
-  if constexpr (VEC == 4 || T >= 2) {
+  if constexpr (PIECES) {
     if ((int)blockIdx.x < piece_blocks) {
       pieces_body<VEC, G, T, U, LDS>(p, (int)blockIdx.x, gl, gbase, gid, stage);
       return;
@@ -741,7 +742,12 @@ hipError_t launch_rg(const Problem& p, hipStream_t s) {
   const int seg_blocks =
       (p.plan && p.nslots > 0) ? std::min(kSegBlocksMax, div_up_host(p.nslots, GPB)) : 0;
   int piece_blocks = 0;
-  if ((VEC == 4 || T >= 2) && p.dp.P > 0) {
+  // Column panels reach the float4 kernels and the scalar ones of N > 64
+  // (per_call_panels, from N = 128).
+  constexpr bool kCanPanel = VEC == 4 || T >= 2;
+  // the segments would skip rows that no piece sums
+  if (!kCanPanel && p.dp.P > 0) return hipErrorInvalidValue;
+  if (kCanPanel && p.dp.P > 0) {
     // chunks of the longest XCD list possible: ceil(P / kXcds) panels x nl_max rows
     const long long per_xcd = (long long)div_up_host(p.dp.P, kXcds) * p.dp.nl_max;
     const long long chunks = (per_xcd + (long long)kPiecesPerGroup * GPB - 1) / ((long long)kPiecesPerGroup * GPB);
@@ -761,9 +767,14 @@ hipError_t launch_rg(const Problem& p, hipStream_t s) {
     const long long blocks = (long long)piece_blocks + (long long)per_launch * slice_blocks;
     if (blocks == 0) return hipSuccess;
     if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((rowgroup_kernel<VEC, G, T, U, LDS>), dim3((unsigned)blocks),
-                       dim3(kWaves * 64), pad_lds, s, p, piece_blocks, seg_blocks, slice_blocks,
-                       s0);
+    if (piece_blocks > 0) {
+      hipLaunchKernelGGL((rowgroup_kernel<VEC, G, T, U, LDS, kCanPanel>), dim3((unsigned)blocks),
+                         dim3(kWaves * 64), pad_lds, s, p, piece_blocks, seg_blocks, slice_blocks,
+                         s0);
+    } else {
+      hipLaunchKernelGGL((rowgroup_kernel<VEC, G, T, U, LDS, false>), dim3((unsigned)blocks),
+                         dim3(kWaves * 64), pad_lds, s, p, 0, seg_blocks, slice_blocks, s0);
+    }
   }
   return hipGetLastError();
 }
