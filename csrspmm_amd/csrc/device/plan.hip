@@ -146,10 +146,10 @@ int build_rowgroup_plan(csrspmm_plan_s* p, const std::vector<int>& rp, int n_hin
   p->mblk = merge_block(vec, M, nnz);
   p->nblocks = merge_blocks(M, nnz, p->mblk);
 
-  // Panelized rows: long, on a large B, with non-decreasing columns.
-  // Only the float4 kernels gain: the scalar-column kernel (one 64-lane group
-  // per row) pays more per piece than it saves.
-  const int P = vec == 4 ? panel_count(K, n_hint) : 0;
+  // Panelized rows: long, on a large B, with non-decreasing columns; for
+  // scalar columns from N = kPanelMinScalarN (measured on XL through a stored
+  // plan: WarpPerRowSmem 625 -> 412 us, WarpPerRow 636 -> 513).
+  const int P = (vec == 4 || n_hint >= kPanelMinScalarN) ? panel_count(K, n_hint) : 0;
   std::vector<int> pan_rows;
   std::vector<int> hcol;
   std::vector<float> hval;
