@@ -94,7 +94,8 @@ void bind_workspace(Problem& p, void* ws, const WorkspaceLayout& L, int mblk) {
 int per_call_panels(int vec, bool plan, int K, int N, int nnz, int hint) {
   if ((vec != 4 && N < kPanelMinScalarN) || !plan || nnz < kPanelMinLen) return 0;
   if (hint >= 0 && hint < kPanelMinLen) return 0;
-  return panel_count(K, N);
+  const int P = panel_count(K, N);
+  return P >= kDevPanelMinPanels ? P : 0;
 }
 
 namespace {

@@ -138,8 +138,8 @@ constexpr long long kPlanMinItems = 1 << 16;
 constexpr int kXcds = 8;
 
 // Column panels.  A row of at least kPanelMinLen nonzeros with sorted
-// columns, on a B of at least 16 MiB with N <= 256 (float4 columns, or scalar
-// ones from N = 128), is cut
+// columns, on a B of at least 16 MiB (per call: at least kDevPanelMinPanels
+// panels) with N <= 256 (float4 columns, or scalar ones from N = 128), is cut
 // at the boundaries of P column panels (P a power of two, kXcds..256, so that
 // a panel's band of B is about kPanelBandBytes).  Each XCD walks its own
 // panels in column order, so the band it gathers from stays in its L2.  Stored
@@ -173,6 +173,20 @@ inline int panel_count(int K, int N) {
   while (p * 2 <= kPanelMaxPanels && p * 2 * kPanelBandBytes <= bbytes) p *= 2;
   return (int)p;
 }
+
+// The per-call path takes panels only when B is wide enough for 32 of them
+// (B >= 64 MiB).  Its pieces are whole (row, panel) ranges: with 8 or 16
+// panels a 16k-nonzero row's pieces are dependent chains of 1-2k nonzeros.
+// Measured on MI355X per call: with 16 panels, power-law rows at K = 65536,
+// N = 128 took 242 us with panels against 194 without, and 278 against 191 at
+// K = 131072, N = 64; with 32 (XL at N = 64, K = 131072 at N = 128) panels
+// won 286 against 350 and 254 against 323.  Stored plans cut pieces at
+// kPieceMaxLen and keep panels from 8 (a 16-panel plan ran 146 us there,
+// 192 without).
+#ifndef CSRSPMM_DEV_PANEL_MIN_PANELS
+#define CSRSPMM_DEV_PANEL_MIN_PANELS 32
+#endif
+constexpr int kDevPanelMinPanels = CSRSPMM_DEV_PANEL_MIN_PANELS;
 
 // Column slices.  On a B much larger than the L2s, gathering one band of sw
 // columns at a time (all rows, then the next band) lets more of the B rows

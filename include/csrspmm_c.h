@@ -86,7 +86,7 @@ size_t csrspmm_workspace_bytes(int algo, int M, int N, int nnz);
 
 /* As csrspmm_workspace_bytes, plus the per-call column-panel tables and
  * partial sums used for rows of >= 1024 nonzeros when B (K x N fp32) is
- * >= 16 MiB and N <= 256, with float4 columns or from N = 128 with scalar
+ * >= 64 MiB and N <= 256, with float4 columns or from N = 128 with scalar
  * ones (at most 256 MiB of partials).  A
  * max_row_nnz_hint in [0, 1024) tells that no such row exists (-1: unknown).
  * csrspmm_spmm_f32_ex given a workspace of at least

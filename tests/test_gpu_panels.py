@@ -1,8 +1,8 @@
 """GPU parity of the per-call column panels.
 
 With float4 columns (WarpPerRowFp4 / WarpPerRowSmemFp4), or scalar ones
-from N = 128 (WarpPerRow / WarpPerRowSmem, Auto), a B of at least 16 MiB and
-N <= 256, every SpMM call cuts rows of >= 1024
+from N = 128 (WarpPerRow / WarpPerRowSmem, Auto), a B wide enough for 32
+panels (>= 64 MiB) and N <= 256, every SpMM call cuts rows of >= 1024
 nonzeros with sorted columns at column-panel boundaries on the device, sums
 the pieces panel by panel (each XCD walking its own panels) and adds a
 row's pieces in column order.  These tests put such rows next to the cases
@@ -26,7 +26,7 @@ PANEL_ALGOS = ["WarpPerRowFp4", "WarpPerRowSmemFp4", "Auto", "WarpPerRow", "Warp
 
 
 def expects_panels(algo, N):
-    """Whether a per-call product on a 16 MiB+ B with N <= 256 takes panels:
+    """Whether a per-call product on a 64 MiB+ B with N <= 256 takes panels:
     float4 columns at any N, scalar columns (Auto below N = 128 included) from
     N = 128."""
     return algo in ("WarpPerRowFp4", "WarpPerRowSmemFp4") or (
@@ -76,9 +76,9 @@ def panel_bytes(algo, M, K, N, nnz):
 @pytest.mark.parametrize("N", [64, 128, 256])
 @pytest.mark.parametrize("algo", list(ALGORITHMS) + ["Auto"])
 def test_panels_mixed_rows(algo, N, gpu):
-    # B of 16 MiB: panels on, and below the 32 MiB from which column slices
-    # take over at N >= 256
-    K = {64: 65536, 128: 32768, 256: 16384}[N]
+    # B of 64 / 64 / 128 MiB: 32 panels or more, and at N = 256 64-column
+    # bands of 32 MiB, too wide for column slices to take over
+    K = {64: 262144, 128: 131072, 256: 131072}[N]
     lens = np.minimum(mixed_lengths(7 + N), K)
     narrow = {int(np.nonzero(lens == 4096)[0][0]): (K // 3, K // 3 + 5000)}  # one panel-ish band
     rowptr, colidx, vals = csr_from_lengths(lens, K, seed=N, narrow=narrow)
@@ -86,7 +86,7 @@ def test_panels_mixed_rows(algo, N, gpu):
     print(f"[panels] mixed {algo} N={N} M={lens.size} nnz={colidx.size}", flush=True)
     base, full = panel_bytes(algo, lens.size, K, N, colidx.size)
     if expects_panels(algo, N):
-        assert full > base, "a 16 MiB B reserves the panel tables"
+        assert full > base, "a 64 MiB B reserves the panel tables"
     else:
         assert full == base
     C = run(algo, rowptr, colidx, vals, B, gpu)
@@ -105,7 +105,7 @@ def test_panels_more_rows_than_the_cap(algo, gpu):
     # 400 rows of 1024..1299 nonzeros: more than the nnz / 4096 rows a call
     # panelizes, so the first ones (in row order) take pieces and the rest
     # segments, in the same call
-    K, N = 32768, 128
+    K, N = 131072, 128
     rng = np.random.default_rng(61)
     lens = rng.integers(0, 20, size=2400)
     lens[rng.choice(lens.size, 400, replace=False)] = rng.integers(1024, 1300, size=400)
@@ -122,7 +122,7 @@ def test_panels_more_rows_than_the_cap(algo, gpu):
 
 @pytest.mark.parametrize("algo", PANEL_ALGOS)
 def test_panels_epilogue_and_strided_b(algo, gpu):
-    K, N = 65536, 128
+    K, N = 131072, 128
     lens = mixed_lengths(21, M=1500)
     rowptr, colidx, vals = csr_from_lengths(lens, K, seed=21)
     Bw = gen.dense(12, gen.TAG_B, K, N + 4)
@@ -140,7 +140,7 @@ def test_panels_epilogue_and_strided_b(algo, gpu):
 
 @pytest.mark.parametrize("algo", PANEL_ALGOS)
 def test_panels_unsorted_row_falls_back(algo, gpu):
-    K, N = 65536, 128
+    K, N = 131072, 128
     lens = mixed_lengths(33)
     r_uns = int(np.nonzero(lens == 5000)[0][0])
     rowptr, colidx, vals = csr_from_lengths(lens, K, seed=33, unsorted_rows={r_uns})
@@ -152,9 +152,9 @@ def test_panels_unsorted_row_falls_back(algo, gpu):
 
 @pytest.mark.parametrize("algo", PANEL_ALGOS)
 def test_panels_skewed_loads_fall_back(algo, gpu):
-    # every long row gathers from the first 1/16 of the columns: two of the
-    # 32 panels carry all the load, so the call keeps the rows on segments
-    K, N = 65536, 128  # 32 panels of 2048 columns
+    # every long row gathers from the first 1/32 of the columns: one of the
+    # 32 panels carries all the load, so the call keeps the rows on segments
+    K, N = 131072, 128  # 32 panels of 4096 columns
     rng = np.random.default_rng(44)
     lens = rng.integers(0, 40, size=3000)
     lens[rng.choice(3000, size=12, replace=False)] = [2048, 2049, 2500, 3000, 3500, 4000] * 2
@@ -168,7 +168,7 @@ def test_panels_skewed_loads_fall_back(algo, gpu):
 
 @pytest.mark.parametrize("algo", PANEL_ALGOS)
 def test_panels_base_workspace_runs_without_panels(algo, gpu):
-    K, N = 65536, 128
+    K, N = 131072, 128
     lens = mixed_lengths(55)
     rowptr, colidx, vals = csr_from_lengths(lens, K, seed=55)
     B = gen.dense(15, gen.TAG_B, K, N)
@@ -185,12 +185,12 @@ def test_panels_base_workspace_runs_without_panels(algo, gpu):
 
 
 @pytest.mark.parametrize("algo", PANEL_ALGOS)
-@pytest.mark.parametrize("K", [50000, 98765])
+@pytest.mark.parametrize("K", [150000, 98765])
 def test_panels_odd_k(algo, K, gpu):
     # K not a power of two: the panel width is ceil(K / P) rounded up to a
     # power of two, so fewer panels than panel_count cover the columns and
     # the last one is partial
-    N = 128 if K == 50000 else 64  # B of 24 / 24 MiB
+    N = 128 if K == 150000 else 256  # B of 73 / 101 MiB: 32 panels
     lens = np.minimum(mixed_lengths(K % 97), K)
     rowptr, colidx, vals = csr_from_lengths(lens, K, seed=K)
     B = gen.dense(16, gen.TAG_B, K, N)
