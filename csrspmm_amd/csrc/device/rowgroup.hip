@@ -349,7 +349,7 @@ __device__ __forceinline__ void pieces_body(const Problem& p, int block, int gl,
 // One block's share of the main launch, over the columns [c_lo, c_hi):
 // block bid < seg_blocks takes long-row segment slots, the others merge
 // blocks of short rows (or, without a plan, rows).
-template <int VEC, int G, int T, int U, bool LDS>
+template <int VEC, int G, int T, int U, bool LDS, int SU>
 __device__ __forceinline__ void rowgroup_block(const Problem& p, int bid, int seg_blocks, int c_lo,
                                                int c_hi, int gl, int gbase, int gid, int2* stage) {
   using VT = typename Vec<VEC>::T;
@@ -358,7 +358,7 @@ __device__ __forceinline__ void rowgroup_block(const Problem& p, int bid, int se
   if (bid < seg_blocks) {
     // Long-row segments, one slot per group (grid-strided if the segment
     // blocks are capped).
-    constexpr int US = CSRSPMM_SEG_UNROLL > U ? (CSRSPMM_SEG_UNROLL < G ? CSRSPMM_SEG_UNROLL : G) : U;
+    constexpr int US = SU > U ? (SU < G ? SU : G) : U;
     for (int s = bid * GPB + gid; s < p.nslots; s += seg_blocks * GPB) {
       const int2 si = p.seg_info[s];
       if (si.x < 0 || si.x >= p.M) continue;  // unused slot
@@ -431,7 +431,7 @@ __device__ __forceinline__ void rowgroup_block(const Problem& p, int bid, int se
 // column panels).  The kernels of calls without them are compiled without
 // that code, which as dead code cost the scalar N <= 64 kernel 9% on R-MAT
 // and the scalar N = 128 / 256 kernels 3-18% on the reference's sweep shapes.
-template <int VEC, int G, int T, int U, bool LDS, bool PIECES>
+template <int VEC, int G, int T, int U, bool LDS, bool PIECES, int SU>
 __global__ __launch_bounds__(kWaves * 64) void rowgroup_kernel(Problem p, int piece_blocks,
                                                                 int seg_blocks, int slice_blocks,
                                                                 int slice0) {
@@ -461,7 +461,7 @@ __global__ __launch_bounds__(kWaves * 64) void rowgroup_kernel(Problem p, int pi
     c_lo = (slice0 + local) * p.sw;
     c_hi = min(p.N, c_lo + p.sw);
   }
-  rowgroup_block<VEC, G, T, U, LDS>(p, bid, seg_blocks, c_lo, c_hi, gl, gbase, gid, stage);
+  rowgroup_block<VEC, G, T, U, LDS, SU>(p, bid, seg_blocks, c_lo, c_hi, gl, gbase, gid, stage);
 }
 
 // Table entries of one row r: the merge-block starts [b_lo, b_hi], the
@@ -734,7 +734,8 @@ void launch_combine(const Problem& p, hipStream_t s) {
   }
 }
 
-template <int VEC, int G, int T, int U, bool LDS>
+// SU: B-row gathers in flight per lane in the long-row segments (at least U).
+template <int VEC, int G, int T, int U, bool LDS, int SU = CSRSPMM_SEG_UNROLL>
 hipError_t launch_rg(const Problem& p, hipStream_t s) {
   constexpr int GPB = kWaves * (64 / G);
   const int units = p.plan ? p.nblocks : p.M;
@@ -768,11 +769,11 @@ hipError_t launch_rg(const Problem& p, hipStream_t s) {
     if (blocks == 0) return hipSuccess;
     if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
     if (piece_blocks > 0) {
-      hipLaunchKernelGGL((rowgroup_kernel<VEC, G, T, U, LDS, kCanPanel>), dim3((unsigned)blocks),
+      hipLaunchKernelGGL((rowgroup_kernel<VEC, G, T, U, LDS, kCanPanel, SU>), dim3((unsigned)blocks),
                          dim3(kWaves * 64), pad_lds, s, p, piece_blocks, seg_blocks, slice_blocks,
                          s0);
     } else {
-      hipLaunchKernelGGL((rowgroup_kernel<VEC, G, T, U, LDS, false>), dim3((unsigned)blocks),
+      hipLaunchKernelGGL((rowgroup_kernel<VEC, G, T, U, LDS, false, SU>), dim3((unsigned)blocks),
                          dim3(kWaves * 64), pad_lds, s, p, 0, seg_blocks, slice_blocks, s0);
     }
   }
@@ -791,6 +792,13 @@ static inline int pow2_ceil(int x) {
 // or all N.
 template <bool LDS>
 static hipError_t dispatch_vec4(const Problem& p, hipStream_t s) {
+  // A column slice (64 columns: 16-lane groups) keeps 8 gathers in flight per
+  // lane in its segments, twice the unsliced kernels'.  Measured on MI355X,
+  // power-law rows (mean 32, rows up to 16k) at N = 256: K = 32768 341 ->
+  // 276 us, K = 65536 325 -> 304; the 66-per-row uniform and R-MAT N = 512
+  // configs within 1%.  Unsliced 16-lane calls keep 4 (XL at N = 64 lost 7%).
+  static_assert(kSliceWidth == 64, "a slice's float4 chunks fill 16-lane groups");
+  if (p.sw == kSliceWidth) return launch_rg<4, 16, 1, kVec4U, LDS, 8>(p, s);
   const int nv = (p.sw > 0 ? std::min(p.sw, p.N) : p.N) / 4;
   const int G = nv >= 64 ? 64 : (pow2_ceil(nv) < 4 ? 4 : pow2_ceil(nv));
   if (G < 64) {
