@@ -23,7 +23,7 @@ at the nominal densities.  rocSPARSE's SpMM (default algorithm, HIP-event
 timed, no per-call synchronisation) is reported beside the C++ sweep as the
 counterpart of the reference's cuSPARSE column.
 
-    python -m csrspmm_amd.reference_sweep --out gpurun_out/sweep --md profiles/reference_sweep.md
+    python -m csrspmm_amd.reference_sweep --out sweep_out --md profiles/reference_sweep.md
 """
 from __future__ import annotations
 
@@ -215,7 +215,7 @@ def markdown(rows, gpu_name, cmd):
 
 def main(argv=None):
     ap = argparse.ArgumentParser()
-    ap.add_argument("--out", default="gpurun_out/reference_sweep", help="directory for the CSV and JSON")
+    ap.add_argument("--out", default="sweep_out", help="directory for the CSV and JSON")
     ap.add_argument("--md", default=None, help="also write the summary here")
     ap.add_argument("--skip-cpp", action="store_true")
     ap.add_argument("--skip-torch", action="store_true")
