@@ -167,3 +167,39 @@ def test_workspace_bytes_ex_panels():
     assert lib.csrspmm_workspace_bytes_ex(a, M, 1024, N, nnz, -1) == base  # B of 512 KiB
     assert lib.csrspmm_workspace_bytes_ex(a, M, K, 512, nnz, -1) == lib.csrspmm_workspace_bytes(a, M, 512, nnz)
     assert lib.csrspmm_workspace_bytes_ex(capi.ALGO["Naive"], M, K, N, nnz, -1) == 0
+
+
+def test_panel_rules_without_device():
+    """The per-call panel decision the host makes (csrspmm_workspace_panel_info):
+    panels need B wide enough for 32 of them (>= 64 MiB), float4 columns or
+    scalar ones from N = 128, no column slices, and a row of >= 1024 nonzeros
+    possible under the hint."""
+    import ctypes
+    lib = capi.hip()
+    A = capi.ALGO
+
+    def panels(algo, M, K, N, nnz, hint=-1):
+        off = ctypes.c_longlong(-1)
+        P = lib.csrspmm_workspace_panel_info(A[algo], M, K, N, nnz, hint, ctypes.byref(off))
+        if P > 0:
+            # the decision word sits inside the workspace the call is sized for
+            assert 0 <= off.value < lib.csrspmm_workspace_bytes_ex(A[algo], M, K, N, nnz, hint)
+        return P
+
+    M, nnz = 262144, 8453223
+    assert panels("WarpPerRowSmemFp4", M, 262144, 128, nnz) == 64    # XL: 128 MiB B
+    assert panels("WarpPerRowSmemFp4", M, 262144, 64, nnz) == 32     # 64 MiB: 32 panels
+    assert panels("WarpPerRowSmemFp4", M, 131072, 64, nnz) == 0      # 32 MiB: 16 panels, too few
+    assert panels("WarpPerRowSmemFp4", M, 65536, 128, nnz) == 0      # 32 MiB
+    assert panels("WarpPerRowSmem", M, 262144, 128, nnz) == 64       # scalar columns from N = 128
+    assert panels("WarpPerRowSmem", M, 262144, 64, nnz) == 0         # but not at N = 64
+    assert panels("Auto", M, 262144, 64, nnz) == 0                   # Auto runs the scalar form there
+    assert panels("Auto", M, 262144, 128, nnz) == 64
+    assert panels("WarpPerRowSmemFp4", M, 65536, 256, nnz) == 0      # 16 MiB bands: column slices
+    assert panels("WarpPerRowSmemFp4", M, 131072, 256, nnz) == 64    # 32 MiB bands: panels
+    assert panels("WarpPerRowSmemFp4", M, 262144, 512, nnz) == 0     # N > 256
+    assert panels("WarpPerRowSmemFp4", M, 262144, 128, nnz, 1023) == 0  # no row of 1024
+    assert panels("WarpPerRowSmemFp4", M, 262144, 128, nnz, 1024) == 64
+    assert panels("Naive", M, 262144, 128, nnz) == 0
+    # K not a power of two: fewer panels than the count, the last one partial
+    assert 16 < panels("WarpPerRowSmemFp4", 3000, 150000, 128, 200000) <= 32
