@@ -47,6 +47,9 @@ HIP_API = {
     "csrspmm_plan_device_bytes": (_c_size_t, [_c_void_p]),
     "csrspmm_plan_panelized_rows": (_c_int, [_c_void_p]),
     "csrspmm_plan_destroy": (_c_int, [_c_void_p]),
+    "csrspmm_release_workspace": (_c_int, [_c_void_p]),
+    "csrspmm_release_all_workspaces": (_c_int, []),
+    "csrspmm_owned_workspaces": (_c_int, [ctypes.POINTER(_c_size_t)]),
     "csrspmm_validate_csr": (_c_int, [_c_int, _c_int, _c_int, _c_void_p, _c_void_p,
                                       ctypes.POINTER(_c_int), ctypes.POINTER(_c_int), _c_void_p]),
     "csrspmm_dense2csr_count_f32": (_c_int, [_c_int, _c_int, _c_void_p, _c_ll, _c_float, _c_void_p,
@@ -138,6 +141,22 @@ def _ptr(t):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
+def leading_dim(X, name="operand") -> int:
+    """Row stride of a 2-D row-major operand (B, C or a dense input):
+    stride(0) whenever X has more than one row, whatever its width, so a
+    one-column view X[:, k:k+1] of a wider tensor is addressed through its
+    parent's rows; max(width, 1) for a single row (or none), whose stride(0)
+    addresses nothing.  A row stride below the width is rejected."""
+    rows, cols = X.shape
+    if rows <= 1:
+        return max(cols, 1)
+    if cols > 1 and X.stride(1) != 1:
+        raise ValueError(f"{name} must be row-major (stride(1) == 1)")
+    if X.stride(0) < max(cols, 1):
+        raise ValueError(f"{name} must have a row stride (stride(0)) of at least its width")
+    return X.stride(0)
+
+
 def spmm(algo, rowptr, colidx, vals, B, C, alpha, beta, *, M=None, K=None, hint=-1, flags=0,
          workspace=None, stream=None, owned_workspace=False):
     """C = alpha*A*B + beta*C through csrspmm_spmm_f32_ex (or csrspmm_spmm_f32
@@ -148,8 +167,8 @@ def spmm(algo, rowptr, colidx, vals, B, C, alpha, beta, *, M=None, K=None, hint=
     K = B.shape[0] if K is None else K
     N = C.shape[1]
     nnz = vals.numel()
-    ldb = B.stride(0) if B.dim() == 2 and B.shape[1] > 1 else max(N, 1)
-    ldc = C.stride(0) if C.shape[1] > 1 else max(N, 1)
+    ldb = leading_dim(B, "B")
+    ldc = leading_dim(C, "C")
     if stream is None:
         stream = torch.cuda.current_stream(C.device).cuda_stream
     lib = hip()
@@ -220,8 +239,8 @@ class Plan:
         if stream is None:
             stream = torch.cuda.current_stream(C.device).cuda_stream
         N = C.shape[1]
-        ldb = B.stride(0) if B.shape[1] > 1 else max(N, 1)
-        ldc = C.stride(0) if N > 1 else max(N, 1)
+        ldb = leading_dim(B, "B")
+        ldc = leading_dim(C, "C")
         check(hip().csrspmm_plan_spmm_f32(self._h, N, _ptr(B), ldb, _ptr(C), ldc, alpha, beta, flags,
                                           ctypes.c_void_p(stream)), "csrspmm_plan_spmm_f32")
         return C
@@ -236,6 +255,25 @@ class Plan:
             self.close()
         except Exception:
             pass
+
+
+def release_workspace(stream=None, device=None) -> None:
+    """Frees the library-owned workspace of (device, stream); the current
+    stream of the current device by default."""
+    if stream is None:
+        stream = torch.cuda.current_stream(device).cuda_stream
+    check(hip().csrspmm_release_workspace(ctypes.c_void_p(stream)), "csrspmm_release_workspace")
+
+
+def release_all_workspaces() -> None:
+    check(hip().csrspmm_release_all_workspaces(), "csrspmm_release_all_workspaces")
+
+
+def owned_workspaces():
+    """(number of library-owned workspaces held, their total bytes)."""
+    b = _c_size_t(0)
+    n = hip().csrspmm_owned_workspaces(ctypes.byref(b))
+    return n, b.value
 
 
 def timing_enable(on: bool) -> None:
@@ -274,7 +312,7 @@ def dense2csr(D, tol=0.0, stream=None):
     s = _stream_of(D, stream)
     rowptr = torch.empty(M + 1, dtype=torch.int32, device=D.device)
     nnz = torch.empty(1, dtype=torch.int64, device=D.device)
-    ld = D.stride(0) if M > 0 and K > 1 else max(K, 1)
+    ld = leading_dim(D, "dense")
     check(hip().csrspmm_dense2csr_count_f32(M, K, _ptr(D), ld, tol, _ptr(rowptr), _ptr(nnz),
                                             ctypes.c_void_p(s)), "csrspmm_dense2csr_count_f32")
     n = int(nnz.item())

@@ -6,6 +6,7 @@
 
 #include <map>
 #include <mutex>
+#include <thread>
 #include <string.h>
 #include <utility>
 #include <vector>
@@ -115,22 +116,85 @@ bool wants_plan(int algo, int M, int nnz, int hint) {
 
 int to_status(hipError_t e) { return e == hipSuccess ? 0 : (int)e; }
 
+// Library-owned workspaces, one per (device, stream).  hipStreamPerThread
+// names a different stream in every host thread, so its workspaces are kept
+// per thread as well.  The map holds at most kMaxOwnedWorkspaces entries; a
+// new key beyond that evicts the least recently used one.
+//
+// Threading: g_ws_mutex is held from the lookup until the call's kernels are
+// enqueued (spmm_impl), so a buffer is never freed between the moment a
+// call takes it and the moment its kernels are queued behind it.  Growing a
+// buffer synchronises its stream first (the stream is alive: its caller is
+// using it); evicting or releasing one synchronises the whole device, since
+// the stream it was keyed on may have been destroyed since.
+struct WsKey {
+  int dev;
+  void* stream;
+  std::thread::id tid;  // set only for hipStreamPerThread
+  bool operator<(const WsKey& o) const {
+    if (dev != o.dev) return dev < o.dev;
+    if (stream != o.stream) return stream < o.stream;
+    return tid < o.tid;
+  }
+};
+
 struct OwnedWorkspace {
   void* ptr = nullptr;
   size_t bytes = 0;
+  unsigned long long last_use = 0;
 };
 
-std::mutex g_ws_mutex;
-std::map<std::pair<int, void*>, OwnedWorkspace> g_ws;
+constexpr size_t kMaxOwnedWorkspaces = 16;
 
-// Grow-only workspace per (device, stream).  Growing waits for the stream so
-// the old buffer is no longer in use when it is freed.
-int owned_workspace(void* stream, size_t bytes, void** out) {
+std::mutex g_ws_mutex;
+std::map<WsKey, OwnedWorkspace> g_ws;
+unsigned long long g_ws_clock = 0;
+
+WsKey ws_key(int dev, void* stream) {
+  WsKey k{dev, stream, std::thread::id()};
+  if (static_cast<hipStream_t>(stream) == hipStreamPerThread) k.tid = std::this_thread::get_id();
+  return k;
+}
+
+// Frees one workspace after all work on its device has finished.  Caller
+// holds g_ws_mutex.
+int free_owned_device_synced(int dev, OwnedWorkspace& w) {
+  if (!w.ptr) return 0;
+  int cur = 0;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) return (int)e;
+  if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return (int)e;
+  e = hipDeviceSynchronize();
+  hipError_t e2 = hipFree(w.ptr);
+  w.ptr = nullptr;
+  w.bytes = 0;
+  hipError_t e3 = cur != dev ? hipSetDevice(cur) : hipSuccess;
+  if (e != hipSuccess) return (int)e;
+  if (e2 != hipSuccess) return (int)e2;
+  return (int)e3;
+}
+
+// The workspace of (current device, stream), grown to at least `bytes`.
+// Caller holds g_ws_mutex until the kernels that use it are enqueued.
+int owned_workspace_locked(void* stream, size_t bytes, void** out) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return (int)e;
-  std::lock_guard<std::mutex> lock(g_ws_mutex);
-  OwnedWorkspace& w = g_ws[std::make_pair(dev, stream)];
+  const WsKey key = ws_key(dev, stream);
+  auto it = g_ws.find(key);
+  if (it == g_ws.end()) {
+    if (g_ws.size() >= kMaxOwnedWorkspaces) {
+      auto lru = g_ws.begin();
+      for (auto j = g_ws.begin(); j != g_ws.end(); ++j)
+        if (j->second.last_use < lru->second.last_use) lru = j;
+      const int st = free_owned_device_synced(lru->first.dev, lru->second);
+      g_ws.erase(lru);
+      if (st != 0) return st;
+    }
+    it = g_ws.emplace(key, OwnedWorkspace{}).first;
+  }
+  OwnedWorkspace& w = it->second;
+  w.last_use = ++g_ws_clock;
   if (w.bytes < bytes) {
     if (w.ptr) {
       e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
@@ -244,6 +308,8 @@ int spmm_impl(int algo_in, int M, int K, int N, int nnz, const int* rowptr, cons
   if (st != 0) return st;
   if (M == 0 || N == 0) return 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // held (owned workspaces only) until the kernels are enqueued
+  std::unique_lock<std::mutex> lock;
   p.plan = wants_plan(algo, M, nnz, hint);
   if (p.plan) {
     const int vec = vector_width(algo, p);
@@ -253,11 +319,12 @@ int spmm_impl(int algo_in, int M, int K, int N, int nnz, const int* rowptr, cons
     if (p.sw > 0) P = 0;  // a sliced call gathers band by band instead
     WorkspaceLayout L = workspace_layout(M, K, N, nnz, P);
     if (owned) {
-      st = owned_workspace(stream, L.total, &ws);
+      lock = std::unique_lock<std::mutex>(g_ws_mutex);
+      st = owned_workspace_locked(stream, L.total, &ws);
       if (st == CSRSPMM_STATUS_ALLOC_FAILED && L.total > L.base_total) {
         // no room for the panel tables: run without them
         L = workspace_layout(M, K, N, nnz, 0);
-        st = owned_workspace(stream, L.total, &ws);
+        st = owned_workspace_locked(stream, L.total, &ws);
       }
       if (st != 0) return st;
     } else {
@@ -448,6 +515,39 @@ int csrspmm_spmm_f32_ex(int algo, int M, int K, int N, int nnz, const int* rowpt
                         void* workspace, size_t workspace_bytes, void* stream) {
   return spmm_impl(algo, M, K, N, nnz, rowptr, colidx, vals, max_row_nnz_hint, B, ldb, C, ldc, alpha,
                    beta, flags, workspace, workspace_bytes, false, stream);
+}
+
+int csrspmm_release_workspace(void* stream) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  std::lock_guard<std::mutex> lock(g_ws_mutex);
+  auto it = g_ws.find(ws_key(dev, stream));
+  if (it == g_ws.end()) return 0;
+  e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+  hipError_t e2 = it->second.ptr ? hipFree(it->second.ptr) : hipSuccess;
+  g_ws.erase(it);
+  if (e != hipSuccess) return (int)e;
+  return to_status(e2);
+}
+
+int csrspmm_release_all_workspaces(void) {
+  std::lock_guard<std::mutex> lock(g_ws_mutex);
+  int st = 0;
+  for (auto& kv : g_ws) {
+    const int s1 = free_owned_device_synced(kv.first.dev, kv.second);
+    if (st == 0) st = s1;
+  }
+  g_ws.clear();
+  return st;
+}
+
+int csrspmm_owned_workspaces(size_t* bytes_out) {
+  std::lock_guard<std::mutex> lock(g_ws_mutex);
+  size_t total = 0;
+  for (const auto& kv : g_ws) total += kv.second.bytes;
+  if (bytes_out) *bytes_out = total;
+  return (int)g_ws.size();
 }
 
 int csrspmm_validate_csr(int M, int K, int nnz, const int* rowptr, const int* colidx, int* flags_out,

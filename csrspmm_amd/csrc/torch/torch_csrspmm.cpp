@@ -24,6 +24,20 @@ using torch::Tensor;
 
 namespace {
 
+// Row stride of a 2-D row-major operand X (B, C or a dense input): stride(0)
+// whenever X has more than one row, whatever its width, so a one-column view
+// such as X[:, k:k+1] of a wider tensor is addressed through its parent's
+// rows; max(width, 1) for a single row (or none), whose stride(0) addresses
+// nothing.  A row stride below the width (overlapping or broadcast rows) is
+// rejected.
+long long leading_dim(const Tensor& X, const char* name) {
+  if (X.size(0) <= 1) return std::max<int64_t>(X.size(1), 1);
+  TORCH_CHECK(X.size(1) <= 1 || X.stride(1) == 1, name, " must be row-major (stride(1) == 1)");
+  TORCH_CHECK(X.stride(0) >= std::max<int64_t>(X.size(1), 1), name,
+              " must have a row stride (stride(0)) of at least its width");
+  return X.stride(0);
+}
+
 void check_inputs(const Tensor& rowptr, const Tensor& colidx, const Tensor& vals, const Tensor& B) {
   TORCH_CHECK(rowptr.is_cuda(), "A_row_ptr must be a CUDA tensor");
   TORCH_CHECK(colidx.is_cuda(), "A_col_idx must be a CUDA tensor");
@@ -65,7 +79,7 @@ Tensor forward(int algo, const Tensor& rowptr, const Tensor& colidx, const Tenso
   Tensor C = torch::empty({M, N}, B.options());
   if (M == 0 || N == 0) return C;
 
-  const long long ldb = B.size(1) <= 1 ? std::max<long long>(N, 1) : B.stride(0);
+  const long long ldb = leading_dim(B, "B");
   const size_t ws_bytes = csrspmm_workspace_bytes_ex(algo, M, K, N, nnz, hint);
   Tensor ws;
   void* ws_ptr = nullptr;
@@ -133,8 +147,6 @@ void check_out(const Tensor& C, const Tensor& B, int64_t M) {
   TORCH_CHECK(C.size(1) <= 1 || C.stride(1) == 1, "C must be row-major (stride(1) == 1)");
 }
 
-long long ld_of(const Tensor& X) { return X.size(1) <= 1 ? std::max<int64_t>(X.size(1), 1) : X.stride(0); }
-
 // C = alpha * A * B + beta * C in place, with the prior C read when beta != 0
 // (the reference's C++ spmm() semantics, src/csrspmm.cpp:28-75; its torch
 // forwards always start from a fresh C).
@@ -155,8 +167,8 @@ Tensor csrspmm_spmm_out(Tensor A_row_ptr, Tensor A_col_idx, Tensor A_values, Ten
   const int st = csrspmm_spmm_f32_ex(a, M, K, N, nnz, A_row_ptr.data_ptr<int>(),
                                      nnz ? A_col_idx.data_ptr<int>() : nullptr,
                                      nnz ? A_values.data_ptr<float>() : nullptr, -1,
-                                     B.numel() ? B.data_ptr<float>() : nullptr, ld_of(B),
-                                     C.data_ptr<float>(), ld_of(C), static_cast<float>(alpha_d),
+                                     B.numel() ? B.data_ptr<float>() : nullptr, leading_dim(B, "B"),
+                                     C.data_ptr<float>(), leading_dim(C, "C"), static_cast<float>(alpha_d),
                                      static_cast<float>(beta_d), 0u,
                                      ws_bytes ? ws.data_ptr() : nullptr, ws_bytes, stream);
   TORCH_CHECK(st == 0, "csrspmm_spmm_out failed: ", csrspmm_status_string(st));
@@ -227,8 +239,8 @@ class CsrSpmmPlan {
     if (C.numel() == 0) return;
     hipStream_t stream = c10::hip::getCurrentHIPStream(B.device().index()).stream();
     const int st = csrspmm_plan_spmm_f32(plan_, static_cast<int>(B.size(1)),
-                                         B.numel() ? B.data_ptr<float>() : nullptr, ld_of(B),
-                                         C.data_ptr<float>(), ld_of(C), static_cast<float>(alpha),
+                                         B.numel() ? B.data_ptr<float>() : nullptr, leading_dim(B, "B"),
+                                         C.data_ptr<float>(), leading_dim(C, "C"), static_cast<float>(alpha),
                                          static_cast<float>(beta), flags, stream);
     TORCH_CHECK(st == 0, "csrspmm plan spmm failed: ", csrspmm_status_string(st));
   }
@@ -257,7 +269,7 @@ std::vector<Tensor> dense_to_csr(Tensor D, double tol) {
   TORCH_CHECK(D.size(0) < INT32_MAX && D.size(1) <= INT32_MAX, "sizes must fit int32");
   c10::DeviceGuard guard(D.device());
   const int M = static_cast<int>(D.size(0)), K = static_cast<int>(D.size(1));
-  const long long ld = K <= 1 ? std::max(K, 1) : D.stride(0);
+  const long long ld = leading_dim(D, "dense");
   Tensor rowptr = torch::empty({M + 1}, D.options().dtype(torch::kInt32));
   Tensor nnz = torch::empty({1}, D.options().dtype(torch::kInt64));
   hipStream_t s = stream_of(D);

@@ -123,6 +123,9 @@ int csrspmm_workspace_panel_info(int algo, int M, int K, int N, int nnz, int max
  * Asynchronous: returns after enqueueing.  Uses a library-owned device
  * workspace kept per (device, stream) and grown on demand; calls on one
  * stream are ordered, calls on different streams use different workspaces.
+ * Thread-safe: a call holds the library's workspace lock until its kernels
+ * are enqueued, so another thread growing or releasing the same workspace
+ * waits for them.
  */
 int csrspmm_spmm_f32(int algo, int M, int K, int N, int nnz,
                      const int* rowptr, const int* colidx, const float* vals,
@@ -131,6 +134,26 @@ int csrspmm_spmm_f32(int algo, int M, int K, int N, int nnz,
                      float* C, long long ldc,
                      float alpha, float beta,
                      void* stream);
+
+/*
+ * Library-owned workspaces (those of csrspmm_spmm_f32).  The library keeps
+ * at most 16 of them (one per device and stream, and per host thread for
+ * hipStreamPerThread), evicting the least recently used one beyond that.
+ * No counterpart in the reference, whose kernels need no workspace.
+ *
+ * csrspmm_release_workspace frees the workspace of (current device, stream)
+ * after synchronising that stream; 0 when there was none.  The next call on
+ * the stream allocates a new one.
+ * csrspmm_release_all_workspaces frees every one of them, on every device,
+ * each after a device synchronise (their streams may no longer exist).
+ * csrspmm_owned_workspaces returns how many are held and, in *bytes_out (may
+ * be NULL), their total size.
+ * All three are safe to call from any thread, concurrently with
+ * csrspmm_spmm_f32 on other streams.
+ */
+int csrspmm_release_workspace(void* stream);
+int csrspmm_release_all_workspaces(void);
+int csrspmm_owned_workspaces(size_t* bytes_out);
 
 /* Flags for csrspmm_spmm_f32_ex. */
 enum {

@@ -203,3 +203,25 @@ def test_panel_rules_without_device():
     assert panels("Naive", M, 262144, 128, nnz) == 0
     # K not a power of two: fewer panels than the count, the last one partial
     assert 16 < panels("WarpPerRowSmemFp4", 3000, 150000, 128, 200000) <= 32
+
+
+def test_leading_dim_rule():
+    """The row stride a tensor operand is passed with: stride(0) for any
+    operand of two rows or more (a one-column view of a wider tensor keeps
+    its parent's row stride), the width for a single row; a row stride below
+    the width, or a non-unit column stride, is rejected."""
+    import torch
+
+    X = torch.zeros(10, 4)
+    assert capi.leading_dim(X) == 4
+    assert capi.leading_dim(X[:, 2:3]) == 4           # one column, strides (4, 1)
+    assert capi.leading_dim(X[:, :3]) == 4            # padded rows
+    assert capi.leading_dim(X[3:4, :3]) == 3          # one row: the width
+    assert capi.leading_dim(torch.zeros(0, 5)) == 5
+    assert capi.leading_dim(torch.zeros(6, 0)) >= 0   # no columns: the call returns early
+    assert capi.leading_dim(torch.zeros(1, 0)) == 1
+    assert capi.leading_dim(torch.zeros(7, 1)) == 1
+    with pytest.raises(ValueError, match="row stride"):
+        capi.leading_dim(torch.zeros(1, 4).expand(3, 4))
+    with pytest.raises(ValueError, match="row-major"):
+        capi.leading_dim(torch.zeros(4, 3).t())
