@@ -39,6 +39,10 @@ HIP_API = {
                                      _c_void_p, _c_int, _c_void_p, _c_ll, _c_void_p, _c_ll,
                                      _c_float, _c_float, ctypes.c_uint, _c_void_p, _c_size_t,
                                      _c_void_p]),
+    "csrspmm_spmm_f32_noalloc": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p,
+                                          _c_void_p, _c_void_p, _c_int, _c_void_p, _c_ll,
+                                          _c_void_p, _c_ll, _c_float, _c_float, ctypes.c_uint,
+                                          _c_void_p]),
     "csrspmm_plan_create": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_void_p, _c_void_p, _c_void_p,
                                      _c_int, _c_void_p, ctypes.POINTER(_c_void_p)]),
     "csrspmm_plan_spmm_f32": (_c_int, [_c_void_p, _c_int, _c_void_p, _c_ll, _c_void_p, _c_ll, _c_float,
@@ -158,10 +162,11 @@ def leading_dim(X, name="operand") -> int:
 
 
 def spmm(algo, rowptr, colidx, vals, B, C, alpha, beta, *, M=None, K=None, hint=-1, flags=0,
-         workspace=None, stream=None, owned_workspace=False):
+         workspace=None, stream=None, owned_workspace=False, noalloc=False):
     """C = alpha*A*B + beta*C through csrspmm_spmm_f32_ex (or csrspmm_spmm_f32
-    when owned_workspace=True).  All tensors on one GPU; C is written in place.
-    Returns C.  Allocates the workspace with torch when none is given."""
+    when owned_workspace=True, csrspmm_spmm_f32_noalloc when noalloc=True).
+    All tensors on one GPU; C is written in place.  Returns C.  Allocates the
+    workspace with torch when none is given (not for noalloc)."""
     a = ALGO[algo] if isinstance(algo, str) else int(algo)
     M = rowptr.numel() - 1 if M is None else M
     K = B.shape[0] if K is None else K
@@ -172,7 +177,11 @@ def spmm(algo, rowptr, colidx, vals, B, C, alpha, beta, *, M=None, K=None, hint=
     if stream is None:
         stream = torch.cuda.current_stream(C.device).cuda_stream
     lib = hip()
-    if owned_workspace:
+    if noalloc:
+        st = lib.csrspmm_spmm_f32_noalloc(a, M, K, N, nnz, _ptr(rowptr), _ptr(colidx), _ptr(vals),
+                                          hint, _ptr(B), ldb, _ptr(C), ldc, alpha, beta, flags,
+                                          ctypes.c_void_p(stream))
+    elif owned_workspace:
         st = lib.csrspmm_spmm_f32(a, M, K, N, nnz, _ptr(rowptr), _ptr(colidx), _ptr(vals), hint,
                                   _ptr(B), ldb, _ptr(C), ldc, alpha, beta, ctypes.c_void_p(stream))
     else:

@@ -298,6 +298,37 @@ hipError_t launch_algorithm(int algo, const Problem& p, hipStream_t s) {
 
 namespace {
 
+// Device scratch of csrspmm_spmm_f32_noalloc: the workspace of its calls,
+// CSRSPMM_NOALLOC_SCRATCH_BYTES per GPU, held by every GPU the library runs
+// on until the process ends.  In host code `scratch` names a host-side
+// stand-in, not device memory: the device address of each GPU's copy comes
+// from hipGetSymbolAddress, taken once per device (with that device
+// current) on its first no-allocation call and kept in g_scratch_ptr; only
+// that address is handed to kernels.  No kernel needs any of it to start at
+// zero: every entry a call reads is written earlier in the same call.
+static __device__ __align__(256) unsigned char scratch[CSRSPMM_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+int scratch_on_current_device(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxScratchDevices) return CSRSPMM_STATUS_NOT_SUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!ptr || (reinterpret_cast<uintptr_t>(ptr) & 255)) return CSRSPMM_STATUS_NOT_SUPPORTED;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
 int spmm_impl(int algo_in, int M, int K, int N, int nnz, const int* rowptr, const int* colidx,
               const float* vals, int hint, const float* B, long long ldb, float* C, long long ldc,
               float alpha, float beta, unsigned flags, void* ws, size_t ws_bytes, bool owned,
@@ -446,6 +477,9 @@ const char* csrspmm_status_string(int status) {
     case CSRSPMM_STATUS_ALLOC_FAILED: return "workspace allocation failed";
     case CSRSPMM_STATUS_INVALID_CSR: return "invalid CSR matrix";
     case CSRSPMM_STATUS_WORKSPACE_TOO_SMALL: return "workspace too small";
+    case CSRSPMM_STATUS_SCRATCH_TOO_SMALL:
+      return "problem needs a larger workspace than the no-allocation scratch holds "
+             "(CSRSPMM_NOALLOC_SCRATCH_BYTES, 128 MiB per GPU)";
     default:
       if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));
       return "unknown status";
@@ -515,6 +549,22 @@ int csrspmm_spmm_f32_ex(int algo, int M, int K, int N, int nnz, const int* rowpt
                         void* workspace, size_t workspace_bytes, void* stream) {
   return spmm_impl(algo, M, K, N, nnz, rowptr, colidx, vals, max_row_nnz_hint, B, ldb, C, ldc, alpha,
                    beta, flags, workspace, workspace_bytes, false, stream);
+}
+
+int csrspmm_spmm_f32_noalloc(int algo, int M, int K, int N, int nnz, const int* rowptr,
+                             const int* colidx, const float* vals, int max_row_nnz_hint,
+                             const float* B, long long ldb, float* C, long long ldc, float alpha,
+                             float beta, unsigned flags, void* stream) {
+  // The base workspace (block starts, segment slots, partials) must fit; the
+  // per-call panel tables are optional: spmm_impl runs without them when the
+  // scratch cannot hold them, as for any workspace of base size.
+  if (csrspmm_workspace_bytes(algo, M, N, nnz) > CSRSPMM_NOALLOC_SCRATCH_BYTES)
+    return CSRSPMM_STATUS_SCRATCH_TOO_SMALL;
+  void* ws = nullptr;
+  const int st = scratch_on_current_device(&ws);
+  if (st != 0) return st;
+  return spmm_impl(algo, M, K, N, nnz, rowptr, colidx, vals, max_row_nnz_hint, B, ldb, C, ldc, alpha,
+                   beta, flags, ws, CSRSPMM_NOALLOC_SCRATCH_BYTES, false, stream);
 }
 
 int csrspmm_release_workspace(void* stream) {

@@ -45,7 +45,9 @@ enum {
     CSRSPMM_STATUS_NOT_SUPPORTED = -2,     /* shape beyond int32 index range */
     CSRSPMM_STATUS_ALLOC_FAILED = -3,      /* library-owned workspace could not grow */
     CSRSPMM_STATUS_INVALID_CSR = -4,       /* validator found a malformed CSR */
-    CSRSPMM_STATUS_WORKSPACE_TOO_SMALL = -5
+    CSRSPMM_STATUS_WORKSPACE_TOO_SMALL = -5,
+    /* csrspmm_spmm_f32_noalloc: the base workspace exceeds its scratch */
+    CSRSPMM_STATUS_SCRATCH_TOO_SMALL = -6
 };
 
 /* Validator result bits (csrspmm_validate_csr). */
@@ -179,6 +181,33 @@ int csrspmm_spmm_f32_ex(int algo, int M, int K, int N, int nnz,
                         unsigned flags,
                         void* workspace, size_t workspace_bytes,
                         void* stream);
+
+/*
+ * As csrspmm_spmm_f32_ex, with no workspace argument and no allocation: no
+ * counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The workspace is a static device array of
+ * CSRSPMM_NOALLOC_SCRATCH_BYTES (128 MiB) in the library, one per GPU, which
+ * each GPU the library runs on holds until the process ends.  A problem whose
+ * base workspace, csrspmm_workspace_bytes(algo, M, N, nnz), exceeds it is
+ * rejected with CSRSPMM_STATUS_SCRATCH_TOO_SMALL before anything is
+ * enqueued; one whose per-call column-panel tables do not fit as well runs
+ * without panels (the same result, more slowly).  The five benchmark
+ * configurations all fit, with their panels.  Calls no hipMalloc or hipFree
+ * (the first call on a device looks the array's address up once).
+ * All calls on one GPU share its array: calls that overlap on one GPU (on
+ * different streams, or from different threads) race and give wrong
+ * results; order them on one stream or synchronise between them.
+ */
+#define CSRSPMM_NOALLOC_SCRATCH_BYTES (128ull << 20)
+int csrspmm_spmm_f32_noalloc(int algo, int M, int K, int N, int nnz,
+                             const int* rowptr, const int* colidx, const float* vals,
+                             int max_row_nnz_hint,
+                             const float* B, long long ldb,
+                             float* C, long long ldc,
+                             float alpha, float beta,
+                             unsigned flags,
+                             void* stream);
 
 /*
  * Stored plans: analyse A once, then multiply it by many B.  No counterpart

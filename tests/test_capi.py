@@ -225,3 +225,16 @@ def test_leading_dim_rule():
         capi.leading_dim(torch.zeros(1, 4).expand(3, 4))
     with pytest.raises(ValueError, match="row-major"):
         capi.leading_dim(torch.zeros(4, 3).t())
+
+
+def test_noalloc_rejects_beyond_scratch_without_device():
+    """The size check runs on the host before any device call: a problem
+    whose base workspace exceeds the 128 MiB scratch is rejected (null
+    pointers are never reached)."""
+    lib = capi.hip()
+    M, K, N, nnz = 1024, 1, 1100, 8_000_000
+    assert lib.csrspmm_workspace_bytes(capi.ALGO["Auto"], M, N, nnz) > 128 << 20
+    st = lib.csrspmm_spmm_f32_noalloc(capi.ALGO["Auto"], M, K, N, nnz, None, None, None, -1, None,
+                                      N, None, N, 1.0, 0.0, 0, None)
+    assert st == -6
+    assert "no-allocation scratch" in lib.csrspmm_status_string(st).decode()
