@@ -8,10 +8,16 @@ two torch.cuda.synchronize() calls, timed with HIP events on the launch
 stream.  Prints ONE JSON line:
   value      GFLOPS = 2*nnz*N / (ms_per_step) for the headline variant
              (Auto by default: the variant the library picks from N)
-  roofline   achieved gather-model GB/s of one SpMM call on the GPU (a HIP
-             event pair around all of the call's launches, recorded by the
-             library on the launch stream, csrspmm_timing_*) against 8 TB/s;
-             traffic = measured HBM bytes per call from profiles/traffic.json
+  roofline   measured HBM bytes of one SpMM call (rocprofv3 FETCH_SIZE and
+             WRITE_SIZE, calibrated on a device copy: profiles/traffic.json)
+             over the GPU time of that call (a HIP event pair around all of
+             the call's launches, recorded by the library on the launch
+             stream, csrspmm_timing_*), against 8 TB/s.  Beside it, never in
+             its place: the compulsory fraction (each distinct B row read
+             once) and the gather-model figure (a full B row per nonzero,
+             above 1 when B is served from L2 or the MALL).  traffic.json
+             records the kernel-source digest it was measured on; a
+             mismatch with the sources being benched is flagged
   modes      per-call median and mean of the headline variant timed alone:
              warm (back to back), api (host clock with a device sync, as the
              reference's spmm() pays) and cold (after a 512 MiB scratch write
@@ -22,7 +28,9 @@ stream.  Prints ONE JSON line:
              time; the headline stays the per-call path, which needs no
              preprocessing of A
   cpu_baseline  the fp32 CSR restatement (oracle/cpu_spmm.c) on the host
-             cores, full matrix, median of a bounded number of reps
+             cores, full matrix, median of a bounded number of reps, on all
+             threads and on one; the CPU model; and the reference's own dense
+             CPU GEMM (src/host/dense_utils.cpp:109-126) on the host config
 The default config is the XL power-law matrix the north-star target is
 stated on.  --gpus N > 1 exits: this build runs on one GPU.
 """
@@ -152,32 +160,90 @@ def time_plan(capi, torch, algo, d, K, N, steps, warmup):
     return plan, build_ms, start.elapsed_time(stop) / steps, main_ms / max(calls, 1)
 
 
+def _median_reps(fn, budget_s, min_reps=3, max_reps=25):
+    """Median seconds of fn() after one warmup: at least min_reps, more while
+    the budget lasts (at most max_reps)."""
+    fn()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < min_reps or (time.perf_counter() < t_end and len(times) < max_reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(a, B, budget_s):
+    """The fp32 CSR restatement of the reference kernels on the host cores
+    (all threads the OpenMP runtime grants, and one), plus the reference's
+    dense CPU GEMM on the host config."""
     import numpy as np
 
     import oracle  # CPU baseline leg only
 
-    C = np.empty((a.M, B.shape[1]), dtype=np.float32)
+    from csrspmm_amd import configs, gen
+
+    N = B.shape[1]
+    C = np.empty((a.M, N), dtype=np.float32)
     threads = oracle.cpu().cpu_spmm_max_threads()
-    oracle.cpu_spmm_f32(a.rowptr, a.colidx, a.vals, B, C, 1.0, 0.0, threads)  # warmup
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 25):
-        t0 = time.perf_counter()
-        oracle.cpu_spmm_f32(a.rowptr, a.colidx, a.vals, B, C, 1.0, 0.0, threads)
-        times.append(time.perf_counter() - t0)
-        if time.perf_counter() > t_end + 30:
-            break
-    t = statistics.median(times)
+    spmm = lambda nt: oracle.cpu_spmm_f32(a.rowptr, a.colidx, a.vals, B, C, 1.0, 0.0, nt)  # noqa: E731
+    t_all, n_all = _median_reps(lambda: spmm(threads), budget_s * 0.6)
+    t_one, n_one = _median_reps(lambda: spmm(1), budget_s * 0.4, min_reps=3, max_reps=5)
+    # the reference's only CPU product: dense O(M*K*N) GEMM, host config
+    host = configs.CONFIGS["host"]
+    ha = host.csr()
+    Ad = np.zeros((ha.M, ha.K), dtype=np.float32)
+    rows = np.repeat(np.arange(ha.M), np.diff(ha.rowptr))
+    Ad[rows, ha.colidx] = ha.vals
+    Bh = gen.dense(host.seed, gen.TAG_B, ha.K, host.N)
+    Ch = np.zeros((ha.M, host.N), dtype=np.float32)
+    t_gemm, n_gemm = _median_reps(lambda: oracle.cpu_dense_gemm(Ad, Bh, Ch, 1.0, 0.0), 1.0,
+                                  min_reps=5, max_reps=20)
+    gf = lambda t: round(2.0 * a.nnz * N / t / 1e9, 3)  # noqa: E731
     return {
-        "value": round(2.0 * a.nnz * B.shape[1] / t / 1e9, 3),
+        "value": gf(t_all),
         "unit": "GFLOPS",
         "cores": threads,
         "kind": "port",
-        "sample": f"full matrix, N={B.shape[1]}, median of {len(times)} reps "
-                  f"({t * 1e3:.1f} ms/rep), fp32 CSR-order fma restatement, OpenMP "
-                  f"schedule(dynamic,64), -O3 -ffast-math",
+        "sample": f"full matrix, N={N}, median of {n_all} reps ({t_all * 1e3:.1f} ms/rep) on "
+                  f"{threads} threads; fp32 CSR-order fma restatement of the reference kernels, "
+                  f"OpenMP schedule(dynamic,64), -O3 -ffast-math -march=x86-64-v3",
+        "cpu_model": cpu_model(),
+        "one_thread": {"value": gf(t_one), "unit": "GFLOPS", "ms": round(t_one * 1e3, 2),
+                       "reps": n_one},
+        "reference_dense_gemm_host": {
+            "what": "the reference's dense_gemm_cpu (src/host/dense_utils.cpp:109-126), 1 thread, "
+                    "on the host config: dense A 1024x1024 (its 10,240 nonzeros and zeros), "
+                    "B 1024x32",
+            "ms": round(t_gemm * 1e3, 3), "reps": n_gemm,
+            "dense_gflops": round(2.0 * ha.M * ha.K * host.N / t_gemm / 1e9, 3),
+            "sparse_equivalent_gflops": round(2.0 * ha.nnz * host.N / t_gemm / 1e9, 4)},
     }
+
+
+def traffic_entry(path, key):
+    """(entry of profiles/traffic.json for key or None, digest matches?)."""
+    from csrspmm_amd import kernel_source_digest
+
+    if not os.path.exists(path):
+        return None, False
+    with open(path) as f:
+        tr = json.load(f)
+    e = tr.get(key)
+    if e is None:
+        return None, False
+    return e, e.get("source_digest") == kernel_source_digest()
 
 
 def main():
@@ -218,15 +284,25 @@ def main():
 
     flops = configs.flops(a.nnz, N)
     balg = configs.bytes_alg(a.M, a.nnz, N, False)
+    U = configs.distinct_columns(a.colidx, a.K)
+    bmin = configs.bytes_min(a.M, a.nnz, N, U, False)
 
-    def figures(ms, main_ms):
-        return {
+    def figures(ms, main_ms, key=None):
+        f = {
             "ms": round(ms, 5),
             "main_kernel_ms": round(main_ms, 5),
             "gflops": round(flops / (ms * 1e-3) / 1e9, 2),
-            "gbs_alg": round(balg / (main_ms * 1e-3) / 1e9, 1),
-            "frac": round(balg / (main_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "compulsory_frac": round(bmin / (main_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "gather_model_gbs": round(balg / (main_ms * 1e-3) / 1e9, 1),
         }
+        if key is not None:
+            e, fresh = traffic_entry(args.traffic_file, key)
+            if e is not None:
+                gbs = e["bytes_per_call"] / (main_ms * 1e-3) / 1e9
+                f["measured_gbs"] = round(gbs, 1)
+                f["measured_frac"] = round(gbs / HBM_PEAK_GBS, 4)
+                f["traffic_current"] = fresh
+        return f
 
     lib = capi.hip()
     resolved = lib.csrspmm_algorithm_name(
@@ -240,10 +316,10 @@ def main():
         names = ALGORITHMS if args.variants == "all" else args.variants.split(",")
         for name in names:
             if name == resolved:
-                variants[name] = figures(ms, main_ms)
+                variants[name] = figures(ms, main_ms, f"{cfg.name}/{args.algo}")
                 continue
             vms, vmain = time_variant(capi, torch, name, d, args.variant_steps, 3)
-            variants[name] = figures(vms, vmain)
+            variants[name] = figures(vms, vmain, f"{cfg.name}/{name}")
             print(f"[bench] {name}: {vms:.4f} ms/call", file=sys.stderr, flush=True)
 
     modes = None
@@ -255,27 +331,46 @@ def main():
     if args.plan_algo != "none":
         plan, build_ms, pms, pmain = time_plan(capi, torch, args.plan_algo, d, a.K, N,
                                                args.variant_steps, 3)
-        plan_fig = {"algo": args.plan_algo, "resolved": plan.algorithm, **figures(pms, pmain),
+        plan_fig = {"algo": args.plan_algo, "resolved": plan.algorithm,
+                    **figures(pms, pmain, f"{cfg.name}/plan{args.plan_algo}"),
                     "build_ms": round(build_ms, 2), "device_bytes": plan.device_bytes,
                     "panelized_rows": plan.panelized_rows}
         plan.close()
         print(f"[bench] plan {plan_fig['resolved']}: {pms:.4f} ms/call, main {pmain:.4f} ms, "
               f"built in {build_ms:.1f} ms", file=sys.stderr, flush=True)
 
-    traffic = None
-    if os.path.exists(args.traffic_file):
-        with open(args.traffic_file) as f:
-            tr = json.load(f)
-        key = f"{cfg.name}/{args.algo}"
-        if key in tr:
-            traffic = tr[key]["bytes_per_call"]
+    from csrspmm_amd import kernel_source_digest
+
+    tr, tr_fresh = traffic_entry(args.traffic_file, f"{cfg.name}/{args.algo}")
+    traffic = tr["bytes_per_call"] if tr is not None else None
 
     cpu = None
     if args.cpu_seconds > 0:
         print("[bench] cpu baseline...", file=sys.stderr, flush=True)
         cpu = cpu_baseline(a, B, args.cpu_seconds)
 
-    achieved = balg / (main_ms * 1e-3) / 1e9
+    t_s = main_ms * 1e-3
+    if traffic is not None:
+        # measured HBM-side bytes of one call over its GPU time
+        achieved, basis = traffic / t_s / 1e9, "measured traffic (rocprofv3 FETCH_SIZE + WRITE_SIZE)"
+    else:
+        achieved, basis = bmin / t_s / 1e9, "compulsory bytes (no traffic measurement for this key)"
+    roofline = {
+        "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "frac_basis": basis,
+        "traffic_source_digest": tr.get("source_digest") if tr else None,
+        "kernel_source_digest": kernel_source_digest(),
+        "traffic_current": bool(tr_fresh),
+        "compulsory_bytes": bmin, "distinct_columns": U,
+        "compulsory_frac": round(bmin / t_s / 1e9 / HBM_PEAK_GBS, 4),
+        "gather_model_bytes": balg,
+        "gather_model_gbs": round(balg / t_s / 1e9, 1),
+        "kernel": f"{resolved}: all launches of one call", "kernel_ms": round(main_ms, 5)}
+    if traffic is not None and not tr_fresh:
+        print("[bench] WARNING: profiles/traffic.json was measured on other kernel sources "
+              f"({roofline['traffic_source_digest']} vs {roofline['kernel_source_digest']})",
+              file=sys.stderr, flush=True)
+
     out = {
         "metric": METRIC,
         "value": round(flops / (ms * 1e-3) / 1e9, 2),
@@ -292,11 +387,8 @@ def main():
         "config": {"workload": cfg.name, "description": cfg.description, "algo": args.algo,
                    "resolved_algo": resolved,
                    "M": a.M, "K": a.K, "N": N, "nnz": a.nnz, "max_row_nnz": a.max_row_nnz,
-                   "alpha": 1.0, "beta": 0.0, "bytes_alg": balg},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "kernel": f"{resolved}: all launches of one call",
-                     "kernel_ms": round(main_ms, 5)},
+                   "alpha": 1.0, "beta": 0.0},
+        "roofline": roofline,
         "cpu_baseline": cpu,
         "modes": modes,
         "variants": variants,

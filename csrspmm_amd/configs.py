@@ -67,5 +67,20 @@ def bytes_alg(M: int, nnz: int, N: int, beta_nonzero: bool = False) -> int:
     return 4 * (M + 1) + 8 * nnz + 4 * nnz * N + 4 * M * N * (2 if beta_nonzero else 1)
 
 
+def bytes_min(M: int, nnz: int, N: int, U: int, beta_nonzero: bool = False) -> int:
+    """Compulsory bytes per SpMM: as bytes_alg, with each of the U distinct
+    referenced B rows read once instead of once per nonzero."""
+    return 4 * (M + 1) + 8 * nnz + 4 * U * N + 4 * M * N * (2 if beta_nonzero else 1)
+
+
+def distinct_columns(colidx, K: int) -> int:
+    """U: the number of distinct column indices of A (the B rows it reads)."""
+    import numpy as np
+
+    if colidx.size == 0:
+        return 0
+    return int(np.count_nonzero(np.bincount(colidx, minlength=K)))
+
+
 def flops(nnz: int, N: int) -> int:
     return 2 * nnz * N

@@ -35,7 +35,7 @@ def main(argv=None):
 
     import torch
 
-    from csrspmm_amd import capi, configs
+    from csrspmm_amd import capi, configs, kernel_source_digest
 
     dev = torch.device("cuda:0")
     cfg = configs.CONFIGS[args.config]
@@ -44,8 +44,11 @@ def main(argv=None):
     t = lambda x: torch.from_numpy(x).to(dev)  # noqa: E731
     rp, ci, va, dB = t(a.rowptr), t(a.colidx), t(a.vals), t(B)
     C = torch.empty((a.M, cfg.N), dtype=torch.float32, device=dev)
+    U = configs.distinct_columns(a.colidx, a.K)
     print(f"[profile_run] {cfg.name} {args.algo} M={a.M} nnz={a.nnz} N={cfg.N} "
-          f"bytes_alg={configs.bytes_alg(a.M, a.nnz, cfg.N)}", flush=True)
+          f"bytes_alg={configs.bytes_alg(a.M, a.nnz, cfg.N)} "
+          f"bytes_min={configs.bytes_min(a.M, a.nnz, cfg.N, U)} U={U} "
+          f"sources={kernel_source_digest()}", flush=True)
     if args.copy_mib:
         n = args.copy_mib * (1 << 20) // 4
         src = torch.ones(n, dtype=torch.float32, device=dev)

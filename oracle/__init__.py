@@ -37,6 +37,7 @@ _ORACLE_API = {
 _CPU_API = {
     "cpu_spmm_max_threads": (_i, []),
     "cpu_spmm_f32": (None, [_i, _i, _vp, _vp, _vp, _vp, _ll, _vp, _ll, _f, _f, _i]),
+    "cpu_dense_gemm": (None, [_i, _i, _i, _f, _f, _vp, _vp, _vp]),
 }
 
 _lib = None
@@ -166,6 +167,14 @@ def dense_init_random_ref(height, width, low=-1.0, high=1.0, sparsity=0.0, integ
     lib().oracle_dense_init_random_ref(_p(out), height, width, low, high, sparsity,
                                        int(integer_values))
     return out
+
+
+def cpu_dense_gemm(A, B, C, alpha, beta):
+    """Timed reference dense CPU GEMM (fast-math build); C updated in place."""
+    M, N = A.shape
+    K = B.shape[1]
+    cpu().cpu_dense_gemm(M, N, K, alpha, beta, _p(A), _p(B), _p(C))
+    return C
 
 
 def cpu_spmm_f32(rowptr, colidx, vals, B, C, alpha, beta, nthreads=0):

@@ -5,6 +5,9 @@
  * src/device/csrspmm_warp_per_row.cu:37-46), rows spread over OpenMP threads
  * with schedule(dynamic, 64).
  *
+ * Also the reference's dense CPU GEMM (src/host/dense_utils.cpp:109-126),
+ * the only CPU product the reference has, timed on the host config.
+ *
  * TEST INFRASTRUCTURE ONLY: bench.py's cpu_baseline leg times it; nothing in
  * the product calls it.  Built with the reference's release flags
  * (-O3 -ffast-math, CMakeLists.txt:23) except -march=native, which is replaced
@@ -36,6 +39,25 @@ EXPORT void cpu_spmm_f32(int M, int N, const int* rowptr, const int* colidx, con
             for (int j = 0; j < N; ++j) c[j] = alpha * acc[j];
         } else {
             for (int j = 0; j < N; ++j) c[j] = fmaf(alpha, acc[j], beta * c[j]);
+        }
+    }
+}
+
+/*
+ * dense_gemm_cpu as the reference writes it (src/host/dense_utils.cpp:109-126),
+ * reference naming: A is M x N, B is N x K, C is M x K; for each output an
+ * fp32 sum over all N in order, zeros included, then C = alpha*sum + beta*C.
+ * Single-threaded, as the reference's.  Timed beside the GPU on the host
+ * config; the strictly rounded restatement that tests pin is
+ * oracle_dense_gemm_cpu in spmm_oracle.c.
+ */
+EXPORT void cpu_dense_gemm(int M, int N, int K, float alpha, float beta, const float* A,
+                           const float* B, float* C) {
+    for (int i = 0; i < M; ++i) {
+        for (int j = 0; j < K; ++j) {
+            float sum = 0.0f;
+            for (int k = 0; k < N; ++k) sum += A[(size_t)i * N + k] * B[(size_t)k * K + j];
+            C[(size_t)i * K + j] = alpha * sum + beta * C[(size_t)i * K + j];
         }
     }
 }
