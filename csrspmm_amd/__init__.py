@@ -5,7 +5,7 @@ fp32 values) and row-major fp32 B and C.
 Surfaces:
   include/csrspmm_c.h         C ABI (libcsrspmm_hip.so: kernels + launch)
   include/csrspmm/*.h         drop-in C++ API of the reference (libcsrspmm.so)
-  csrspmm_amd.torch_csrspmm   drop-in torch entry points (torch_csrspmm/_C)
+  torch_csrspmm (top level)   drop-in torch entry points (torch_csrspmm/_C)
   csrspmm_amd.capi            ctypes view of the C ABI (tests, benchmarks)
   csrspmm_amd.gen / configs   seeded synthetic inputs and the benchmark configs
 """

@@ -3,11 +3,13 @@
     python -m csrspmm_amd.build            # all targets
     python -m csrspmm_amd.build hip host   # selected targets
 
-Targets (outputs under csrspmm_amd/lib/ and csrspmm_amd/torch_csrspmm/):
+Targets (outputs under csrspmm_amd/lib/ and the top-level torch_csrspmm/):
   hip    libcsrspmm_hip.so   hipcc --offload-arch=gfx950: the kernels + C ABI
   host   libcsrspmm.so       g++: C++ API (include/csrspmm/*), generators
-  torch  torch_csrspmm/_C.so g++: PyTorch-ROCm extension over the C ABI
+  torch  torch_csrspmm/_C.so g++: PyTorch-ROCm extension over the C ABI (the same
+                             module setup.py's CppExtension builds)
   apps   test_csrspmm, bench_csrspmm   g++: C++ drivers over libcsrspmm.so
+         test_kernels_h                 hipcc: launches the kernels of <csrspmm/kernels.h>
   vendor libcsrspmm_vendor.so g++: rocSPARSE SpMM timing shim (comparison bench only)
 """
 from __future__ import annotations
@@ -26,7 +28,7 @@ LIB = os.path.join(PKG, "lib")
 INC = os.path.join(ROOT, "include")
 
 HIP_SOURCES = ["device/capi.hip", "device/rowgroup.hip", "device/naive.hip", "device/plan.hip",
-               "device/panels.hip", "device/csr_tools.hip"]
+               "device/panels.hip", "device/csr_tools.hip", "device/kernels_direct.hip"]
 HOST_SOURCES = ["host/csrspmm.cpp", "host/spmm_launcher.cpp", "host/csr_utils.cpp",
                 "host/dense_utils.cpp", "host/gen.cpp"]
 
@@ -88,7 +90,7 @@ def build_torch() -> str:
     import torch
     from torch.utils import cpp_extension
 
-    outdir = os.path.join(PKG, "torch_csrspmm")
+    outdir = os.path.join(ROOT, "torch_csrspmm")
     out = os.path.join(outdir, "_C" + sysconfig.get_config_var("EXT_SUFFIX"))
     incs = cpp_extension.include_paths(device_type="cuda") + [sysconfig.get_paths()["include"], INC]
     libdirs = cpp_extension.library_paths(device_type="cuda")
@@ -104,7 +106,7 @@ def build_torch() -> str:
         cmd += ["-L", d]
     cmd += ["-L", LIB, "-lcsrspmm_hip", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu",
             "-ltorch_hip", "-ltorch_python",
-            "-Wl,-rpath,$ORIGIN/../lib", "-o", out + ".tmp"]
+            "-Wl,-rpath,$ORIGIN/../csrspmm_amd/lib", "-o", out + ".tmp"]
     _run(cmd)
     os.replace(out + ".tmp", out)
     return out
@@ -118,6 +120,12 @@ def build_apps() -> list[str]:
               "-L", LIB, "-lcsrspmm", "-lcsrspmm_hip", "-Wl,-rpath,$ORIGIN", "-o", out + ".tmp"])
         os.replace(out + ".tmp", out)
         outs.append(out)
+    # HIP code that includes <csrspmm/kernels.h> and launches the kernels itself
+    out = os.path.join(LIB, "test_kernels_h")
+    _run([_hipcc(), *HIPCC_FLAGS, "-I", INC, os.path.join(CSRC, "apps", "test_kernels_h.hip"),
+          "-L", LIB, "-lcsrspmm_hip", "-Wl,-rpath,$ORIGIN", "-o", out + ".tmp"])
+    os.replace(out + ".tmp", out)
+    outs.append(out)
     return outs
 
 

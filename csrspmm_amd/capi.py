@@ -149,10 +149,11 @@ def leading_dim(X, name="operand") -> int:
     """Row stride of a 2-D row-major operand (B, C or a dense input):
     stride(0) whenever X has more than one row, whatever its width, so a
     one-column view X[:, k:k+1] of a wider tensor is addressed through its
-    parent's rows; max(width, 1) for a single row (or none), whose stride(0)
-    addresses nothing.  A row stride below the width is rejected."""
+    parent's rows; max(width, 1) for a single row (or none) or no columns,
+    where stride(0) addresses nothing.  A row stride below the width is
+    rejected."""
     rows, cols = X.shape
-    if rows <= 1:
+    if rows <= 1 or cols == 0:
         return max(cols, 1)
     if cols > 1 and X.stride(1) != 1:
         raise ValueError(f"{name} must be row-major (stride(1) == 1)")

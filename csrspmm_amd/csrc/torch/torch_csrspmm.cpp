@@ -27,11 +27,11 @@ namespace {
 // Row stride of a 2-D row-major operand X (B, C or a dense input): stride(0)
 // whenever X has more than one row, whatever its width, so a one-column view
 // such as X[:, k:k+1] of a wider tensor is addressed through its parent's
-// rows; max(width, 1) for a single row (or none), whose stride(0) addresses
-// nothing.  A row stride below the width (overlapping or broadcast rows) is
-// rejected.
+// rows; max(width, 1) for a single row (or none) or no columns, where
+// stride(0) addresses nothing.  A row stride below the width (overlapping or
+// broadcast rows) is rejected.
 long long leading_dim(const Tensor& X, const char* name) {
-  if (X.size(0) <= 1) return std::max<int64_t>(X.size(1), 1);
+  if (X.size(0) <= 1 || X.size(1) == 0) return std::max<int64_t>(X.size(1), 1);
   TORCH_CHECK(X.size(1) <= 1 || X.stride(1) == 1, name, " must be row-major (stride(1) == 1)");
   TORCH_CHECK(X.stride(0) >= std::max<int64_t>(X.size(1), 1), name,
               " must have a row stride (stride(0)) of at least its width");

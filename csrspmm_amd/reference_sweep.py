@@ -9,7 +9,7 @@ library's drop-in surfaces.
   A is M x N sparse, B is N x K.  The reference's own table is the mean over
   the 20 shapes (README.md:80-88).
 * torch sweep -- reference torch_csrspmm/torch_benchmarks.py: the five torch
-  forwards of csrspmm_amd.torch_csrspmm, plus torch.sparse.mm / addmm, over
+  forwards of torch_csrspmm, plus torch.sparse.mm / addmm, over
   its 4 shapes x 5 densities (A is M x K with a Bernoulli(density) mask, B is
   K x N), alpha 1.1, beta 0.5, each call host-timed with a synchronisation,
   mean of 100 after 20 warmups, GFLOPS = 2 nnz N / t (torch_benchmarks.py:
@@ -110,7 +110,7 @@ def make_vendor_ctx(torch):
 
 
 def torch_sweep(torch, out_rows):
-    from csrspmm_amd import torch_csrspmm as tc
+    import torch_csrspmm as tc
 
     dev = torch.device("cuda:0")
     torch.manual_seed(0)
@@ -192,7 +192,7 @@ def markdown(rows, gpu_name, cmd):
     mt = means(rows, "torch")
     if mt:
         out += ["## Python API (reference torch_csrspmm/torch_benchmarks.py, README \"Python API Performance\")",
-                "", "The five `csrspmm_amd.torch_csrspmm` forwards and `torch.sparse` (on ROCm), host-timed "
+                "", "The five `torch_csrspmm` forwards and `torch.sparse` (on ROCm), host-timed "
                 "with a synchronisation per call, mean of 100 after 20 warmups; mean GFLOPS (2·nnz·N/t) "
                 "over the 20 shapes.", "",
                 "| function | mean GFLOPS here | published (RTX 4070) | ratio |", "|---|---|---|---|"]

@@ -5,6 +5,11 @@
 #include <csrspmm/config.h>
 #include <csrspmm/csr_utils.h>
 #include <csrspmm/matrix.h>
+#if defined(__HIPCC__) || defined(__HIP__)
+// HIP code also sees the kernel declarations, as the reference's csrspmm.h:6
+// gives them (other compilers cannot parse __global__).
+#include <csrspmm/kernels.h>
+#endif
 
 struct csrspmm_plan_s;  // opaque plan of the C ABI (include/csrspmm_c.h)
 

@@ -218,7 +218,8 @@ def test_leading_dim_rule():
     assert capi.leading_dim(X[:, :3]) == 4            # padded rows
     assert capi.leading_dim(X[3:4, :3]) == 3          # one row: the width
     assert capi.leading_dim(torch.zeros(0, 5)) == 5
-    assert capi.leading_dim(torch.zeros(6, 0)) >= 0   # no columns: the call returns early
+    assert capi.leading_dim(torch.zeros(6, 0)) == 1   # no columns: nothing to address
+    assert capi.leading_dim(torch.from_numpy(__import__("numpy").zeros((5, 0), "f4"))) == 1
     assert capi.leading_dim(torch.zeros(1, 0)) == 1
     assert capi.leading_dim(torch.zeros(7, 1)) == 1
     with pytest.raises(ValueError, match="row stride"):
@@ -238,3 +239,18 @@ def test_noalloc_rejects_beyond_scratch_without_device():
                                       N, None, N, 1.0, 0.0, 0, None)
     assert st == -6
     assert "no-allocation scratch" in lib.csrspmm_status_string(st).decode()
+
+
+def test_kernels_h_symbols_exported():
+    """The reference's six kernel declarations (include/csrspmm/kernels.h)
+    have their host-side launch stubs in libcsrspmm_hip.so, so HIP code that
+    declares and launches them links against the library."""
+    header = open(os.path.join(os.path.dirname(LIB_DIR), "..", "include", "csrspmm",
+                               "kernels.h")).read()
+    names = re.findall(r"__global__ void (\w+)\(", header)
+    assert len(names) == 6
+    out = __import__("subprocess").run(["nm", "-D", "--defined-only",
+                                        os.path.join(LIB_DIR, "libcsrspmm_hip.so")],
+                                       capture_output=True, text=True, check=True).stdout
+    for n in names:
+        assert re.search(rf"_ZN7csrspmm6kernel\d+__device_stub__{n}E", out), n

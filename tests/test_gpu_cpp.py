@@ -35,3 +35,17 @@ def test_cpp_bench_driver(gpu):
     assert r.returncode == 0, r.stderr
     m = re.search(r"performance: \(\s*([0-9.]+)\) GFLOPS", r.stdout)
     assert m and float(m.group(1)) > 0
+
+
+def test_kernels_h_direct_launches(gpu):
+    """HIP code that includes <csrspmm/kernels.h> (reference
+    include/csrspmm/kernels.h:6-71) and launches the six kernels itself, with
+    the reference launcher's shapes and others, checked element by element
+    against an fp64 product inside the driver."""
+    r = subprocess.run([os.path.join(LIB_DIR, "test_kernels_h")], capture_output=True, text=True,
+                       timeout=120)
+    print(r.stdout, r.stderr)
+    assert r.returncode == 0
+    # 6 kernels x (2 or 3 launch shapes) x 3 column counts
+    assert r.stdout.count(" ok ") == 3 * (2 * 2 + 4 * 3)
+    assert "FAIL" not in r.stdout

@@ -19,15 +19,40 @@ test_gpu_parity.py cover the values themselves.
   the bound on a small case), where the sampled rows might miss it.  Small
   value errors are left to the sampled oracle rows and the identities.
 """
+import functools
+
 import numpy as np
 import pytest
 import torch
 
-from csrspmm_amd import capi, configs
+from csrspmm_amd import ALGORITHMS, capi, configs
 
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-5
+
+
+@functools.lru_cache(maxsize=None)
+def matrix(cfg_name):
+    return configs.CONFIGS[cfg_name].csr()
+
+
+@functools.lru_cache(maxsize=2)
+def colsum_closed_form(cfg_name):
+    """(want, bound) per output column, fp64, from A's column sums and B."""
+    cfg = configs.CONFIGS[cfg_name]
+    a = matrix(cfg_name)
+    B = cfg.B(a.K)
+    vals = a.vals.astype(np.float64)
+    w = np.bincount(a.colidx, weights=vals, minlength=a.K)
+    w_abs = np.bincount(a.colidx, weights=np.abs(vals), minlength=a.K)
+    want = np.zeros(cfg.N)
+    bound = np.zeros(cfg.N)
+    for k0 in range(0, a.K, 65536):  # B in fp64 a band of rows at a time
+        Bk = B[k0:k0 + 65536].astype(np.float64)
+        want += w[k0:k0 + 65536] @ Bk
+        bound += w_abs[k0:k0 + 65536] @ np.abs(Bk)
+    return want, bound
 
 
 def dev_t(a, dev):
@@ -41,11 +66,11 @@ def spmm(algo, drp, dci, dva, dB, M, alpha=1.0):
     return C
 
 
-@pytest.mark.parametrize("algo", ["Auto", "WarpPerRow"])
+@pytest.mark.parametrize("algo", ("Auto",) + ALGORITHMS)
 @pytest.mark.parametrize("cfg_name", ["xl", "large", "rmat512"])
 def test_exact_identities(cfg_name, algo, gpu):
     cfg = configs.CONFIGS[cfg_name]
-    a = cfg.csr()
+    a = matrix(cfg_name)
     print(f"[fullsize] identities {cfg_name} {algo} M={a.M} nnz={a.nnz} N={cfg.N}", flush=True)
     drp, dci, dva = dev_t(a.rowptr, gpu), dev_t(a.colidx, gpu), dev_t(a.vals, gpu)
     dB = dev_t(cfg.B(a.K), gpu)
@@ -62,26 +87,23 @@ def test_exact_identities(cfg_name, algo, gpu):
     assert torch.equal(C4, C * 0.5), "alpha = 0.5 is not C / 2 bit for bit"
 
 
-@pytest.mark.parametrize("cfg_name", ["xl", "xl98", "rmat", "large"])
+@pytest.mark.parametrize("cfg_name", ["xl", "xl98", "rmat", "rmat512", "large"])
 def test_column_checksums(cfg_name, gpu):
+    """Every variant (and Auto) on the full matrix: each output column's sum
+    against the closed form."""
     cfg = configs.CONFIGS[cfg_name]
-    a = cfg.csr()
-    print(f"[fullsize] checksums {cfg_name} M={a.M} nnz={a.nnz} N={cfg.N}", flush=True)
-    B = cfg.B(a.K)
-    C = spmm("Auto", dev_t(a.rowptr, gpu), dev_t(a.colidx, gpu), dev_t(a.vals, gpu), dev_t(B, gpu), a.M)
-    got = C.double().sum(0).cpu().numpy()
-    vals = a.vals.astype(np.float64)
-    w = np.bincount(a.colidx, weights=vals, minlength=a.K)
-    w_abs = np.bincount(a.colidx, weights=np.abs(vals), minlength=a.K)
-    want = np.zeros(cfg.N)
-    bound = np.zeros(cfg.N)
-    for k0 in range(0, a.K, 65536):  # B in fp64 a band of rows at a time
-        Bk = B[k0:k0 + 65536].astype(np.float64)
-        want += w[k0:k0 + 65536] @ Bk
-        bound += w_abs[k0:k0 + 65536] @ np.abs(Bk)
-    err = np.abs(got - want)
-    assert (err <= TOL * bound).all(), \
-        f"{cfg_name}: column sums off, worst {np.max(err / bound):.3g} of the 1e-5 bound"
+    a = matrix(cfg_name)
+    want, bound = colsum_closed_form(cfg_name)
+    drp, dci, dva = dev_t(a.rowptr, gpu), dev_t(a.colidx, gpu), dev_t(a.vals, gpu)
+    dB = dev_t(cfg.B(a.K), gpu)
+    for algo in ("Auto",) + ALGORITHMS:
+        print(f"[fullsize] checksums {cfg_name} {algo} M={a.M} nnz={a.nnz} N={cfg.N}", flush=True)
+        C = spmm(algo, drp, dci, dva, dB, a.M)
+        got = C.double().sum(0).cpu().numpy()
+        del C
+        err = np.abs(got - want)
+        assert (err <= TOL * bound).all(), \
+            f"{cfg_name} {algo}: column sums off, worst {np.max(err / bound):.3g} of the 1e-5 bound"
 
 
 @pytest.mark.parametrize("cfg_name,algo,expect", [
@@ -92,7 +114,7 @@ def test_panel_decision(cfg_name, algo, expect, gpu):
     configs (columns uniform) panelize every row of >= 1024 nonzeros, all
     under the nnz / 4096 cap; R-MAT's hot columns read as skewed."""
     cfg = configs.CONFIGS[cfg_name]
-    a = cfg.csr()
+    a = matrix(cfg_name)
     print(f"[fullsize] panel decision {cfg_name} {algo}", flush=True)
     C = torch.empty((a.M, cfg.N), device=gpu)
     nl = capi.panelized_rows(algo, dev_t(a.rowptr, gpu), dev_t(a.colidx, gpu), dev_t(a.vals, gpu),

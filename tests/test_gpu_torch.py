@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 import torch
 
-import csrspmm_amd.torch_csrspmm as tc
+import torch_csrspmm as tc
 import oracle
 from csrspmm_amd import configs
 

@@ -7,7 +7,7 @@ import inspect
 import pytest
 import torch
 
-import csrspmm_amd.torch_csrspmm as tc
+import torch_csrspmm as tc
 
 SIGS = {
     "csrspmm_naive": ["A_rowptr", "A_colidx", "A_values", "B", "alpha", "beta"],
@@ -66,3 +66,24 @@ def test_sparse_csr_entry_checks_on_host():
         tc.from_sparse_csr(torch.eye(3))
     with pytest.raises(RuntimeError, match="CUDA"):
         tc.dense_to_csr(torch.eye(3))
+
+
+def test_import_name_and_setup_extension():
+    """`import torch_csrspmm` resolves to the top-level package of this tree
+    (the reference's import name, torch_csrspmm/__init__.py:1-7), and
+    setup.py declares its extension as the reference's setup.py does
+    (setup.py:79-86: torch_csrspmm._C), built from the committed C++ source
+    against the in-tree kernel library (a CppExtension: no CUDA, no hipify)."""
+    import importlib.util
+    import os
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    assert os.path.dirname(tc.__file__) == os.path.join(root, "torch_csrspmm")
+    spec = importlib.util.spec_from_file_location("csrspmm_setup", os.path.join(root, "setup.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)  # the setup() call is guarded by __main__
+    (ext,) = mod.ext_modules()
+    assert ext.name == "torch_csrspmm._C"
+    assert all(os.path.exists(os.path.join(root, s)) for s in ext.sources)
+    assert "csrspmm_hip" in ext.libraries
+    assert not any("cuda" in s.lower() for s in ext.sources)

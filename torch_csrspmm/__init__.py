@@ -1,14 +1,17 @@
-"""Drop-in for the reference's ``torch_csrspmm`` package
-(reference torch_csrspmm/__init__.py:10-23): the same five entry points with
-the same argument order, each returning a new ``[M, N]`` fp32 tensor with B's
-options, computed by the gfx950 HIP kernels of ``libcsrspmm_hip.so``.
+"""Drop-in for the reference's ``torch_csrspmm`` package, under its import
+name (reference torch_csrspmm/__init__.py:1-23): the same five entry points
+with the same argument order, each returning a new ``[M, N]`` fp32 tensor with
+B's options, computed by the gfx950 HIP kernels of ``libcsrspmm_hip.so``.
 
-    import csrspmm_amd.torch_csrspmm as torch_csrspmm
+    import torch_csrspmm
     C = torch_csrspmm.csrspmm_warp_per_row_fp4(rowptr, colidx, vals, B, alpha, beta)
 
-The launch goes on the current HIP stream of B's device and is asynchronous.
-There is no CPU path: importing this module raises if the extension is not
-built (``python -m csrspmm_amd.build``).
+The extension ``torch_csrspmm._C`` is built in place by
+``python -m csrspmm_amd.build`` or ``python setup.py build_ext --inplace``
+(after ``python -m csrspmm_amd.build hip``, which builds the kernels it
+links).  The launch goes on the current HIP stream of B's device and is
+asynchronous.  There is no CPU path: importing this module raises if the
+extension is not built.
 """
 import torch  # noqa: F401  (loads torch's HIP runtime before the extension binds to it)
 
@@ -16,7 +19,7 @@ try:
     from . import _C
 except ImportError as exc:  # pragma: no cover - exercised only when the build is missing
     raise ImportError(
-        "csrspmm_amd.torch_csrspmm: the HIP extension _C is not built; run "
+        "torch_csrspmm: the HIP extension _C is not built; run "
         "`python -m csrspmm_amd.build` (needs hipcc for gfx950)") from exc
 
 __all__ = [
