@@ -84,6 +84,36 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 __device__ __forceinline__ int clamp_nnz(int x, int nnz) { return min(max(x, 0), nnz); }
 
+// B through a buffer resource (BUF kernels): a gather's byte offset
+// row * ldb * 4 + column * 4 is one 32-bit v_mad_u32_u24 instead of 64-bit
+// address arithmetic, and the hardware range-checks it against B's extent (an
+// offset at or past the end reads 0 and fetches nothing).  The host picks BUF
+// only when B's extent is at most kBufMaxBytes and rows and row lengths fit
+// 24 bits (buf_gathers_ok), so a valid offset stays below kBufOffPast and an
+// offset of kBufOffPast or more, plus any column byte offset, still lies past
+// the end without wrapping.
+constexpr unsigned kBufOffPast = 0xC0000000u;
+struct BufB {
+  __amdgpu_buffer_rsrc_t rsrc;
+  unsigned rowbytes;
+};
+__device__ __forceinline__ BufB make_bufb(const Problem& p) {
+  BufB bb;
+  const long long bytes = p.K > 0 ? (long long)(p.K - 1) * p.ldb * 4 + (long long)p.N * 4 : 0;
+  bb.rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p.B), (short)0,
+                                              (int)(bytes < (long long)kBufOffPast ? bytes : 0), 0x00020000);
+  bb.rowbytes = (unsigned)(p.ldb * 4);
+  return bb;
+}
+template <int VEC>
+__device__ __forceinline__ typename Vec<VEC>::T ld_b_buf(const BufB& bb, unsigned off) {
+  if constexpr (VEC == 4) {
+    return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(bb.rsrc, (int)off, 0, 0));
+  } else {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(bb.rsrc, (int)off, 0, 0));
+  }
+}
+
 // True when this call's column panels took the long row starting at
 // nonzero x0 (its segments are then skipped).
 __device__ __forceinline__ bool is_panelized(const Problem& p, int x0) {
@@ -94,18 +124,24 @@ __device__ __forceinline__ bool is_panelized(const Problem& p, int x0) {
   return pi >= 0 && pi < p.dp.sched[0];
 }
 
-// Column bookkeeping of one panel of PW = G*VEC*T columns starting at c0.
-template <int VEC, int G, int T>
+// Column bookkeeping of one panel of PW = G*VEC*T columns starting at c0;
+// with BUF, B's buffer resource and each column's byte offset in a B row
+// (past the buffer for a column at or beyond climit, so it fetches nothing).
+template <int VEC, int G, int T, bool BUF>
 struct Panel {
   const float* bcol[T];
   bool cval[T];
   int col[T];
+  unsigned colbytes[T];
+  BufB bb;
   __device__ __forceinline__ Panel(const Problem& p, int c0, int gl, int climit) {
+    if constexpr (BUF) bb = make_bufb(p);
 #pragma unroll
     for (int t = 0; t < T; ++t) {
       col[t] = c0 + (gl + G * t) * VEC;
       cval[t] = col[t] < climit;  // VEC == 4 requires N % 4 == 0 (host-checked)
       bcol[t] = p.B + col[t];
+      colbytes[t] = cval[t] ? (unsigned)col[t] * 4u : kBufOffPast;
     }
   }
 };
@@ -113,44 +149,84 @@ struct Panel {
 // One chunk of up to G nonzeros [base, base + cnt): broadcast each (col, val)
 // to the group, gather U B-row slices at a time, and hand every product to
 // `consume(j, v, b)` in CSR order (j = nonzero index).
-template <int VEC, int G, int T, int U, bool LDS, class Consume>
-__device__ __forceinline__ void chunk_gather(const Problem& p, const Panel<VEC, G, T>& pn, int base,
-                                             int cnt, int cj, float vj, int gl, int gbase,
+template <int VEC, int G, int T, int U, bool LDS, bool BUF, class Consume>
+__device__ __forceinline__ void chunk_gather(const Problem& p, const Panel<VEC, G, T, BUF>& pn,
+                                             int base, int cnt, int cj, float vj, int gl, int gbase,
                                              int2* stage, Consume&& consume) {
   using VT = typename Vec<VEC>::T;
   if constexpr (LDS) {
     stage[gbase + gl] = make_int2(cj, __float_as_int(vj));
     wave_lds_sync();
   }
-  for (int k = 0; k < cnt; k += U) {
-    int c[U];
-    float v[U];
+  // (col, val) of entry kk of the chunk; kk < G
+  auto pair = [&](int kk, int& c, float& v) {
+    if constexpr (LDS) {
+      const int2 e = stage[gbase + kk];
+      c = e.x;
+      v = __int_as_float(e.y);
+    } else {
+      c = group_bcast<G>(cj, gbase, kk);
+      v = group_bcast<G>(vj, gbase, kk);
+    }
+  };
+  if constexpr (BUF) {
+    // Full batches of U need no per-entry masks; the last, partial batch
+    // gives its missing entries an offset past the buffer and skips them.
+    // k is a multiple of U below cnt <= G, so k + u < G.
+    int k = 0;
+    for (; k + U <= cnt; k += U) {
+      int c[U];
+      float v[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int kk = (k + u) & (G - 1);
-      if constexpr (LDS) {
-        const int2 e = stage[gbase + kk];
-        c[u] = e.x;
-        v[u] = __int_as_float(e.y);
-      } else {
-        c[u] = group_bcast<G>(cj, gbase, kk);
-        v[u] = group_bcast<G>(vj, gbase, kk);
+      for (int u = 0; u < U; ++u) pair(k + u, c[u], v[u]);
+      VT b[U][T];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const unsigned roff = __umul24((unsigned)c[u], pn.bb.rowbytes);
+#pragma unroll
+        for (int t = 0; t < T; ++t) b[u][t] = ld_b_buf<VEC>(pn.bb, roff + pn.colbytes[t]);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) consume(base + k + u, v[u], b[u]);
+    }
+    if (k < cnt) {
+      int c[U];
+      float v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) pair(k + u, c[u], v[u]);
+      VT b[U][T];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const unsigned roff = (k + u) < cnt ? __umul24((unsigned)c[u], pn.bb.rowbytes) : kBufOffPast;
+#pragma unroll
+        for (int t = 0; t < T; ++t) b[u][t] = ld_b_buf<VEC>(pn.bb, roff + pn.colbytes[t]);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if ((k + u) < cnt) consume(base + k + u, v[u], b[u]);
       }
     }
-    VT b[U][T];
+  } else {
+    for (int k = 0; k < cnt; k += U) {
+      int c[U];
+      float v[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const bool ok = (k + u) < cnt;
-      const long long roff = (long long)c[u] * p.ldb;
+      for (int u = 0; u < U; ++u) pair((k + u) & (G - 1), c[u], v[u]);
+      VT b[U][T];
 #pragma unroll
-      for (int t = 0; t < T; ++t) {
-        b[u][t] = Vec<VEC>::zero();
-        if (ok && pn.cval[t]) b[u][t] = ld_b<VEC>(pn.bcol[t] + roff);
+      for (int u = 0; u < U; ++u) {
+        const bool ok = (k + u) < cnt;
+        const long long roff = (long long)c[u] * p.ldb;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          b[u][t] = Vec<VEC>::zero();
+          if (ok && pn.cval[t]) b[u][t] = ld_b<VEC>(pn.bcol[t] + roff);
+        }
       }
-    }
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if ((k + u) < cnt) consume(base + k + u, v[u], b[u]);
+      for (int u = 0; u < U; ++u) {
+        if ((k + u) < cnt) consume(base + k + u, v[u], b[u]);
+      }
     }
   }
   if constexpr (LDS) wave_lds_sync();
@@ -170,8 +246,8 @@ __device__ __forceinline__ void load_chunk(const Problem& p, int j0, int end, in
 // Walks nonzeros [start, end) in chunks of G with the next chunk's (col, val)
 // prefetched, calling consume(j, v, b[T]) for each in order; (cj, vj) is the
 // caller's load of the first chunk.
-template <int VEC, int G, int T, int U, bool LDS, class Consume>
-__device__ __forceinline__ void stream_nonzeros_from(const Problem& p, const Panel<VEC, G, T>& pn,
+template <int VEC, int G, int T, int U, bool LDS, bool BUF, class Consume>
+__device__ __forceinline__ void stream_nonzeros_from(const Problem& p, const Panel<VEC, G, T, BUF>& pn,
                                                      int start, int end, int cj, float vj, int gl,
                                                      int gbase, int2* stage, Consume&& consume) {
   for (int base = start; base < end; base += G) {
@@ -182,21 +258,21 @@ __device__ __forceinline__ void stream_nonzeros_from(const Problem& p, const Pan
       cn = ld_stream(p.colidx + jn);
       vn = ld_stream(p.vals + jn);
     }
-    chunk_gather<VEC, G, T, U, LDS>(p, pn, base, min(G, end - base), cj, vj, gl, gbase, stage,
+    chunk_gather<VEC, G, T, U, LDS, BUF>(p, pn, base, min(G, end - base), cj, vj, gl, gbase, stage,
                                     consume);
     cj = cn;
     vj = vn;
   }
 }
 
-template <int VEC, int G, int T, int U, bool LDS, class Consume>
-__device__ __forceinline__ void stream_nonzeros(const Problem& p, const Panel<VEC, G, T>& pn,
+template <int VEC, int G, int T, int U, bool LDS, bool BUF, class Consume>
+__device__ __forceinline__ void stream_nonzeros(const Problem& p, const Panel<VEC, G, T, BUF>& pn,
                                                 int start, int end, int gl, int gbase, int2* stage,
                                                 Consume&& consume) {
   int cj;
   float vj;
   load_chunk(p, start, end, gl, cj, vj);
-  stream_nonzeros_from<VEC, G, T, U, LDS>(p, pn, start, end, cj, vj, gl, gbase, stage, consume);
+  stream_nonzeros_from<VEC, G, T, U, LDS, BUF>(p, pn, start, end, cj, vj, gl, gbase, stage, consume);
 }
 
 template <int VEC, int T>
@@ -213,8 +289,8 @@ __device__ __forceinline__ void store_row(const Problem& p, int row, const int (
 // Short rows [rs, re) streamed: windows of up to G consecutive rows whose
 // nonzeros form one contiguous range; a row longer than kLongRow ends the
 // window and is skipped (its segments are summed elsewhere).
-template <int VEC, int G, int T, int U, bool LDS>
-__device__ __forceinline__ void stream_rows(const Problem& p, const Panel<VEC, G, T>& pn, int rs,
+template <int VEC, int G, int T, int U, bool LDS, bool BUF>
+__device__ __forceinline__ void stream_rows(const Problem& p, const Panel<VEC, G, T, BUF>& pn, int rs,
                                             int re, int gl, int gbase, int2* stage) {
   using VT = typename Vec<VEC>::T;
   const unsigned long long gmask = G == 64 ? ~0ULL : (((1ULL << G) - 1ULL) << gbase);
@@ -236,7 +312,7 @@ __device__ __forceinline__ void stream_rows(const Problem& p, const Panel<VEC, G
       VT acc[T];
 #pragma unroll
       for (int t = 0; t < T; ++t) acc[t] = Vec<VEC>::zero();
-      stream_nonzeros<VEC, G, T, U, LDS>(
+      stream_nonzeros<VEC, G, T, U, LDS, BUF>(
           p, pn, jb, je, gl, gbase, stage, [&](int j, float v, const VT(&b)[T]) {
             // rows ending before nonzero j are complete (je bounds cur < nb)
             while (j >= cur_end) {
@@ -266,7 +342,7 @@ __device__ __forceinline__ void stream_rows(const Problem& p, const Panel<VEC, G
 // grid covers nl_max rows (the host cannot know nl); chunks past the list
 // exit at once, and they come last.  The short-row and segment blocks follow
 // in the same grid and take over slots as the pieces run out.
-template <int VEC, int G, int T, int U, bool LDS>
+template <int VEC, int G, int T, int U, bool LDS, bool BUF>
 __device__ __forceinline__ void pieces_body(const Problem& p, int block, int gl, int gbase, int gid,
                                             int2* stage) {
   using VT = typename Vec<VEC>::T;
@@ -309,11 +385,11 @@ __device__ __forceinline__ void pieces_body(const Problem& p, int block, int gl,
     }
     const int q = qa + (int)(i / (unsigned)nl);
     float* prow = d.part + ((long long)(i % (unsigned)nl) * d.P + q) * p.ldp;
-    const Panel<VEC, G, T> pn0(p, 0, gl, p.N);
+    const Panel<VEC, G, T, BUF> pn0(p, 0, gl, p.N);
     VT acc[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) acc[t] = Vec<VEC>::zero();
-    stream_nonzeros_from<VEC, G, T, UP, LDS>(p, pn0, a, e, cj, vj, gl, gbase, stage,
+    stream_nonzeros_from<VEC, G, T, UP, LDS, BUF>(p, pn0, a, e, cj, vj, gl, gbase, stage,
                                              [&](int, float v, const VT(&bv)[T]) {
 #pragma unroll
                                                for (int t = 0; t < T; ++t) acc[t] = fma_v(v, bv[t], acc[t]);
@@ -325,10 +401,10 @@ __device__ __forceinline__ void pieces_body(const Problem& p, int block, int gl,
     }
     // columns beyond the first PW (N > G * VEC * T): the rest of the piece, plainly
     for (int c0 = PW; c0 < p.N; c0 += PW) {
-      const Panel<VEC, G, T> pn(p, c0, gl, p.N);
+      const Panel<VEC, G, T, BUF> pn(p, c0, gl, p.N);
 #pragma unroll
       for (int t = 0; t < T; ++t) acc[t] = Vec<VEC>::zero();
-      stream_nonzeros<VEC, G, T, UP, LDS>(p, pn, a, e, gl, gbase, stage,
+      stream_nonzeros<VEC, G, T, UP, LDS, BUF>(p, pn, a, e, gl, gbase, stage,
                                           [&](int, float v, const VT(&bv)[T]) {
 #pragma unroll
                                             for (int t = 0; t < T; ++t) acc[t] = fma_v(v, bv[t], acc[t]);
@@ -349,7 +425,7 @@ __device__ __forceinline__ void pieces_body(const Problem& p, int block, int gl,
 // One block's share of the main launch, over the columns [c_lo, c_hi):
 // block bid < seg_blocks takes long-row segment slots, the others merge
 // blocks of short rows (or, without a plan, rows).
-template <int VEC, int G, int T, int U, bool LDS, int SU>
+template <int VEC, int G, int T, int U, bool LDS, bool BUF, int SU>
 __device__ __forceinline__ void rowgroup_block(const Problem& p, int bid, int seg_blocks, int c_lo,
                                                int c_hi, int gl, int gbase, int gid, int2* stage) {
   using VT = typename Vec<VEC>::T;
@@ -373,11 +449,11 @@ __device__ __forceinline__ void rowgroup_block(const Problem& p, int bid, int se
       // from the clamped row range, so this stays inside the buffer)
       float* prow = p.partials + ((long long)(clamp_nnz(rs, p.nnz) >> p.seg_shift) + si.y) * p.ldp;
       for (int c0 = c_lo; c0 < c_hi; c0 += PW) {
-        const Panel<VEC, G, T> pn(p, c0, gl, c_hi);
+        const Panel<VEC, G, T, BUF> pn(p, c0, gl, c_hi);
         VT acc[T];
 #pragma unroll
         for (int t = 0; t < T; ++t) acc[t] = Vec<VEC>::zero();
-        stream_nonzeros<VEC, G, T, US, LDS>(p, pn, start, end, gl, gbase, stage,
+        stream_nonzeros<VEC, G, T, US, LDS, BUF>(p, pn, start, end, gl, gbase, stage,
                                             [&](int, float v, const VT(&b)[T]) {
 #pragma unroll
                                               for (int t = 0; t < T; ++t) acc[t] = fma_v(v, b[t], acc[t]);
@@ -402,8 +478,8 @@ __device__ __forceinline__ void rowgroup_block(const Problem& p, int bid, int se
     const int rs = max(0, p.block_start[unit]);
     const int re = min(p.M, p.block_start[unit + 1]);
     for (int c0 = c_lo; c0 < c_hi; c0 += PW) {
-      const Panel<VEC, G, T> pn(p, c0, gl, c_hi);
-      stream_rows<VEC, G, T, U, LDS>(p, pn, rs, re, gl, gbase, stage);
+      const Panel<VEC, G, T, BUF> pn(p, c0, gl, c_hi);
+      stream_rows<VEC, G, T, U, LDS, BUF>(p, pn, rs, re, gl, gbase, stage);
     }
     return;
   }
@@ -414,11 +490,11 @@ __device__ __forceinline__ void rowgroup_block(const Problem& p, int bid, int se
   const int start = p.rowptr[row];
   const int end = p.rowptr[row + 1];
   for (int c0 = c_lo; c0 < c_hi; c0 += PW) {
-    const Panel<VEC, G, T> pn(p, c0, gl, c_hi);
+    const Panel<VEC, G, T, BUF> pn(p, c0, gl, c_hi);
     VT acc[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) acc[t] = Vec<VEC>::zero();
-    stream_nonzeros<VEC, G, T, U, LDS>(p, pn, start, end, gl, gbase, stage,
+    stream_nonzeros<VEC, G, T, U, LDS, BUF>(p, pn, start, end, gl, gbase, stage,
                                        [&](int, float v, const VT(&b)[T]) {
 #pragma unroll
                                          for (int t = 0; t < T; ++t) acc[t] = fma_v(v, b[t], acc[t]);
@@ -431,7 +507,7 @@ __device__ __forceinline__ void rowgroup_block(const Problem& p, int bid, int se
 // column panels).  The kernels of calls without them are compiled without
 // that code, which as dead code cost the scalar N <= 64 kernel 9% on R-MAT
 // and the scalar N = 128 / 256 kernels 3-18% on the reference's sweep shapes.
-template <int VEC, int G, int T, int U, bool LDS, bool PIECES, int SU>
+template <int VEC, int G, int T, int U, bool LDS, bool PIECES, int SU, bool BUF>
 __global__ __launch_bounds__(kWaves * 64) void rowgroup_kernel(Problem p, int piece_blocks,
                                                                 int seg_blocks, int slice_blocks,
                                                                 int slice0) {
@@ -447,7 +523,7 @@ __global__ __launch_bounds__(kWaves * 64) void rowgroup_kernel(Problem p, int pi
 
   if constexpr (PIECES) {
     if ((int)blockIdx.x < piece_blocks) {
-      pieces_body<VEC, G, T, U, LDS>(p, (int)blockIdx.x, gl, gbase, gid, stage);
+      pieces_body<VEC, G, T, U, LDS, BUF>(p, (int)blockIdx.x, gl, gbase, gid, stage);
       return;
     }
   }
@@ -461,7 +537,7 @@ __global__ __launch_bounds__(kWaves * 64) void rowgroup_kernel(Problem p, int pi
     c_lo = (slice0 + local) * p.sw;
     c_hi = min(p.N, c_lo + p.sw);
   }
-  rowgroup_block<VEC, G, T, U, LDS, SU>(p, bid, seg_blocks, c_lo, c_hi, gl, gbase, gid, stage);
+  rowgroup_block<VEC, G, T, U, LDS, BUF, SU>(p, bid, seg_blocks, c_lo, c_hi, gl, gbase, gid, stage);
 }
 
 // Table entries of one row r: the merge-block starts [b_lo, b_hi], the
@@ -735,7 +811,8 @@ void launch_combine(const Problem& p, hipStream_t s) {
 }
 
 // SU: B-row gathers in flight per lane in the long-row segments (at least U).
-template <int VEC, int G, int T, int U, bool LDS, int SU = CSRSPMM_SEG_UNROLL>
+// BUF: B gathered through a buffer resource (buf_gathers_ok must hold).
+template <int VEC, int G, int T, int U, bool LDS, int SU = CSRSPMM_SEG_UNROLL, bool BUF = false>
 hipError_t launch_rg(const Problem& p, hipStream_t s) {
   constexpr int GPB = kWaves * (64 / G);
   const int units = p.plan ? p.nblocks : p.M;
@@ -769,11 +846,11 @@ hipError_t launch_rg(const Problem& p, hipStream_t s) {
     if (blocks == 0) return hipSuccess;
     if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
     if (piece_blocks > 0) {
-      hipLaunchKernelGGL((rowgroup_kernel<VEC, G, T, U, LDS, kCanPanel, SU>), dim3((unsigned)blocks),
+      hipLaunchKernelGGL((rowgroup_kernel<VEC, G, T, U, LDS, kCanPanel, SU, BUF>), dim3((unsigned)blocks),
                          dim3(kWaves * 64), pad_lds, s, p, piece_blocks, seg_blocks, slice_blocks,
                          s0);
     } else {
-      hipLaunchKernelGGL((rowgroup_kernel<VEC, G, T, U, LDS, false, SU>), dim3((unsigned)blocks),
+      hipLaunchKernelGGL((rowgroup_kernel<VEC, G, T, U, LDS, false, SU, BUF>), dim3((unsigned)blocks),
                          dim3(kWaves * 64), pad_lds, s, p, 0, seg_blocks, slice_blocks, s0);
     }
   }
@@ -788,8 +865,47 @@ static inline int pow2_ceil(int x) {
   return v;
 }
 
+// Unsliced float4 calls: the group width from N.
+template <bool LDS, bool BUF>
+static hipError_t dispatch_vec4_cols(const Problem& p, hipStream_t s) {
+  constexpr int SU = CSRSPMM_SEG_UNROLL;
+  const int nv = p.N / 4;
+  const int G = nv >= 64 ? 64 : (pow2_ceil(nv) < 4 ? 4 : pow2_ceil(nv));
+  if (G < 64) {
+    switch (G) {
+      case 4: return launch_rg<4, 4, 1, kVec4U, LDS, SU, BUF>(p, s);
+      case 8: return launch_rg<4, 8, 1, kVec4U, LDS, SU, BUF>(p, s);
+      case 16: return launch_rg<4, 16, 1, kVec4U, LDS, SU, BUF>(p, s);
+      default: return launch_rg<4, 32, 1, kVec4U, LDS, SU, BUF>(p, s);
+    }
+  }
+  const int t = (nv + 63) / 64;
+  if (t <= 1) return launch_rg<4, 64, 1, kVec4U, LDS, SU, BUF>(p, s);
+  if (t <= 2) return launch_rg<4, 64, 2, 4, LDS, SU, BUF>(p, s);
+  return launch_rg<4, 64, 4, 2, LDS, SU, BUF>(p, s);  // N > 1024 loops over 1024-column panels
+}
+
+// B can be gathered through a buffer resource: every row and row length fits
+// 24 bits (one v_mad_u32_u24 per offset) and B's extent stays below
+// kBufOffPast.
+static bool buf_gathers_ok(const Problem& p) {
+  if (p.K <= 0 || p.K >= (1 << 24) || p.ldb * 4 >= (1LL << 24)) return false;
+  const long long bytes = (long long)(p.K - 1) * p.ldb * 4 + (long long)p.N * 4;
+  return bytes < (long long)kBufOffPast;
+}
+
 // The kernel shape comes from the columns one block covers: a column slice,
 // or all N.
+//
+// Unsliced float4 calls gather B through a buffer resource when it fits
+// (buf_gathers_ok).  Measured on MI355X against 64-bit global loads, with
+// bit-identical results: XL 393.6 -> 376.3 us per call (VALU instructions
+// 133 M -> 59 M, L2 hit rate 0.50 -> 0.56, fetched bytes -12%), the
+// mean-98 power-law config 1085 -> 1071 us, medium 48.5 -> 45.1 us.  Sliced
+// calls keep global loads: the 65536 x 256 uniform config went 381 -> 423 us
+// with the same L2 requests and its hit rate falling 0.48 -> 0.39 (leaner
+// waves keep more rows of its 16 MiB band in flight), and 399 us at 4 or 5
+// blocks per CU; R-MAT N = 512 was unchanged.
 template <bool LDS>
 static hipError_t dispatch_vec4(const Problem& p, hipStream_t s) {
   // A column slice (64 columns: 16-lane groups) keeps 8 gathers in flight per
@@ -799,20 +915,8 @@ static hipError_t dispatch_vec4(const Problem& p, hipStream_t s) {
   // configs within 1%.  Unsliced 16-lane calls keep 4 (XL at N = 64 lost 7%).
   static_assert(kSliceWidth == 64, "a slice's float4 chunks fill 16-lane groups");
   if (p.sw == kSliceWidth) return launch_rg<4, 16, 1, kVec4U, LDS, 8>(p, s);
-  const int nv = (p.sw > 0 ? std::min(p.sw, p.N) : p.N) / 4;
-  const int G = nv >= 64 ? 64 : (pow2_ceil(nv) < 4 ? 4 : pow2_ceil(nv));
-  if (G < 64) {
-    switch (G) {
-      case 4: return launch_rg<4, 4, 1, kVec4U, LDS>(p, s);
-      case 8: return launch_rg<4, 8, 1, kVec4U, LDS>(p, s);
-      case 16: return launch_rg<4, 16, 1, kVec4U, LDS>(p, s);
-      default: return launch_rg<4, 32, 1, kVec4U, LDS>(p, s);
-    }
-  }
-  const int t = (nv + 63) / 64;
-  if (t <= 1) return launch_rg<4, 64, 1, kVec4U, LDS>(p, s);
-  if (t <= 2) return launch_rg<4, 64, 2, 4, LDS>(p, s);
-  return launch_rg<4, 64, 4, 2, LDS>(p, s);  // N > 1024 loops over 1024-column panels
+  if (buf_gathers_ok(p)) return dispatch_vec4_cols<LDS, true>(p, s);
+  return dispatch_vec4_cols<LDS, false>(p, s);
 }
 
 template <bool LDS>

@@ -225,7 +225,10 @@ inline int slice_width(int K, int N, bool panels) {
 // the cap cost 22%, so it stops there.  The cap is set by padding each
 // block's LDS so that only kSliceBlocksPerCu fit in the CU's kLdsPerCu.
 constexpr long long kSliceCapBand = 8LL << 20;
-constexpr int kSliceBlocksPerCu = 6;
+#ifndef CSRSPMM_SLICE_BLOCKS_PER_CU
+#define CSRSPMM_SLICE_BLOCKS_PER_CU 6
+#endif
+constexpr int kSliceBlocksPerCu = CSRSPMM_SLICE_BLOCKS_PER_CU;
 constexpr int kLdsPerCu = 160 * 1024;
 inline int slice_blocks_per_cu(int K, int sw, bool slice_launch) {
   if (sw <= 0 || !slice_launch || (long long)K * sw * 4 <= kSliceCapBand) return 0;
