@@ -507,6 +507,53 @@ __device__ __forceinline__ void rowgroup_block(const Problem& p, int bid, int se
   }
 }
 
+// The main launch with column panels holds piece_blocks pieces blocks (a
+// multiple of kXcds) and the blocks of the other roles (segments, merge
+// blocks).  The pieces gather from an L2-resident band and are bound by L2
+// bandwidth; the other roles gather at random and are bound by L2 misses.
+// Run back to back on XL they take 161 + 182 us; interleaved, they overlap.
+// Grid block b belongs to group b / kXcds (one block per XCD); the groups
+// cycle through kInterPieces groups of pieces blocks, then kInterRest groups
+// of the other roles, until one role runs out, and the rest of the grid is
+// the remaining role.  Pieces block i keeps running on XCD i mod kXcds.
+// Measured on MI355X per call (float4 columns; ratio pieces : other):
+//   XL         pieces first 369.5 us, 1:1 419.7, 2:1 349.2, 3:2 346.7,
+//              4:3 345.3, 5:4 344.9, 3:1 387.2, 4:1 362.3
+//   XL-98      1073.2 us -> 1002.7 (4:3)
+//   power-law rows, K = 131072, N = 128: 198.4 -> 192.5 us (4:3)
+// A cycle of 4 groups (3:1, and 1:1 at 2) put the other roles' blocks on the
+// same CUs of each XCD every time; 4:3 cycles through 7.  Scalar-column
+// calls keep the pieces first: interleaved, XL WarpPerRow went 514 -> 523 us.
+constexpr int kInterPieces = 4;
+constexpr int kInterRest = 3;
+__device__ __forceinline__ void interleave_roles(int b, int piece_blocks, int total, int& piece,
+                                                 int& other) {
+  const int pg = piece_blocks / kXcds;
+  const int rg = (total - piece_blocks) / kXcds;
+  const int g = b / kXcds, x = b % kXcds;
+  constexpr int kCycle = kInterPieces + kInterRest;
+  const int cycles = min(pg / kInterPieces, rg / kInterRest);
+  if (g < cycles * kCycle) {
+    const int c = g / kCycle, k = g % kCycle;
+    if (k < kInterPieces) {
+      piece = (c * kInterPieces + k) * kXcds + x;
+    } else {
+      piece = -1;
+      other = (c * kInterRest + (k - kInterPieces)) * kXcds + x;
+    }
+    return;
+  }
+  // past the cycles: the remaining pieces blocks, then the remaining others
+  const int t = (g - cycles * kCycle) * kXcds + x;
+  const int pdone = cycles * kInterPieces * kXcds;
+  if (pdone + t < piece_blocks) {
+    piece = pdone + t;
+  } else {
+    piece = -1;
+    other = cycles * kInterRest * kXcds + (pdone + t - piece_blocks);
+  }
+}
+
 // PIECES: compiled with the panel pieces (launched only for calls with
 // column panels).  The kernels of calls without them are compiled without
 // that code, which as dead code cost the scalar N <= 64 kernel 9% on R-MAT
@@ -525,15 +572,21 @@ __global__ __launch_bounds__(kWaves * 64) void rowgroup_kernel(Problem p, int pi
   __shared__ int2 stage_all[LDS ? kWaves * 64 : 1];
   int2* stage = stage_all + (LDS ? wave * 64 : 0);
 
+  int bid = (int)blockIdx.x - piece_blocks;
   if constexpr (PIECES) {
-    if ((int)blockIdx.x < piece_blocks) {
-      pieces_body<VEC, G, T, U, LDS, BUF>(p, (int)blockIdx.x, gl, gbase, gid, stage);
+    int piece = -1;
+    if constexpr (VEC == 4) {
+      interleave_roles((int)blockIdx.x, piece_blocks, (int)gridDim.x, piece, bid);
+    } else if ((int)blockIdx.x < piece_blocks) {
+      piece = (int)blockIdx.x;
+    }
+    if (piece >= 0) {
+      pieces_body<VEC, G, T, U, LDS, BUF>(p, piece, gl, gbase, gid, stage);
       return;
     }
   }
   // Column slices: the blocks of slice sl cover columns [c_lo, c_hi), and a
   // launch holds one slice or all of them in slice order (launch_rg).
-  int bid = (int)blockIdx.x - piece_blocks;
   int c_lo = 0, c_hi = p.N;
   if (p.sw > 0) {
     const int local = bid / slice_blocks;  // bid counts from this launch's first slice, slice0
