@@ -221,10 +221,13 @@ int owned_workspace_locked(void* stream, size_t bytes, void** out) {
 
 int resolve_algorithm(int algo, int N) {
   if (algo == CSRSPMM_ALGO_AUTO) {
-    // Measured on MI355X: the LDS-staged warp-per-row forms lead on every
-    // config; float4 columns win from N = 128 up, scalar columns below
-    // (64-lane groups instead of 16-lane float4 groups).
-    return (N % 4 == 0 && N >= 128) ? CSRSPMM_ALGO_WARP_PER_ROW_SMEM_FP4 : CSRSPMM_ALGO_WARP_PER_ROW_SMEM;
+    // Measured on MI355X: float4 columns win from N = 128 up, scalar columns
+    // below (64-lane groups instead of 16-lane float4 groups), where the
+    // LDS-staged form leads.  From N = 128 the broadcast form is ahead on the
+    // power-law configs (XL 341.1 -> 333.9 us, the mean-98 config 988 ->
+    // 957 us), 1.7% behind on power-law rows at K = 131072, and within 0.3%
+    // on the uniform and R-MAT configs.
+    return (N % 4 == 0 && N >= 128) ? CSRSPMM_ALGO_WARP_PER_ROW_FP4 : CSRSPMM_ALGO_WARP_PER_ROW_SMEM;
   }
   if (algo < 0 || algo >= CSRSPMM_ALGO_COUNT) return -1;
   return algo;

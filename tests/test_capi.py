@@ -44,8 +44,8 @@ def test_parse_and_names():
     assert lib.csrspmm_algorithm_name(6).decode() == "Auto"
     assert lib.csrspmm_algorithm_name(7) is None
     # Auto resolves by N; concrete ids pass through
-    assert lib.csrspmm_resolve_algorithm(6, 128) == 5
-    assert lib.csrspmm_resolve_algorithm(6, 256) == 5
+    assert lib.csrspmm_resolve_algorithm(6, 128) == 3
+    assert lib.csrspmm_resolve_algorithm(6, 256) == 3
     assert lib.csrspmm_resolve_algorithm(6, 64) == 4
     assert lib.csrspmm_resolve_algorithm(6, 130) == 4
     assert lib.csrspmm_resolve_algorithm(2, 128) == 2

@@ -28,7 +28,7 @@ def test_plan_configs(cfg_name, algo, gpu):
     rp, ci, va = dev_t(a.rowptr, gpu), dev_t(a.colidx, gpu), dev_t(a.vals, gpu)
     plan = capi.Plan(algo, rp, ci, va, a.K, n_hint=cfg.N)
     if algo == "Auto":
-        assert plan.algorithm == ("WarpPerRowSmemFp4" if cfg.N >= 128 else "WarpPerRowSmem")
+        assert plan.algorithm == ("WarpPerRowFp4" if cfg.N >= 128 else "WarpPerRowSmem")
     rows = sample_rows(a, cfg_name in ("host", "medium"))
     concrete = plan.algorithm
     C1 = plan_run(plan, B, gpu, a.M, cfg.N)

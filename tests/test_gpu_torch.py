@@ -144,7 +144,7 @@ def test_plan_class(gpu):
     B = cfg.B(a.K)
     t = lambda x: torch.from_numpy(x).to(gpu)  # noqa: E731
     plan = tc.CsrSpmmPlan(t(a.rowptr), t(a.colidx), t(a.vals), a.K, n_hint=cfg.N)
-    assert plan.algorithm == "WarpPerRowSmemFp4" and plan.panelized_rows > 0
+    assert plan.algorithm == "WarpPerRowFp4" and plan.panelized_rows > 0
     assert plan.device_bytes > 0
     rows = np.unique(np.concatenate([np.argsort(np.diff(a.rowptr))[-32:],
                                      np.arange(0, a.M, 97)])).astype(np.int32)
