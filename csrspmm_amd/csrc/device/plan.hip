@@ -20,6 +20,17 @@
 // into a partial buffer; the combine pass adds a row's pieces in column
 // order.  Measured on the XL config, in isolation, this cut the long-row
 // part from 562 us to 352 us.
+//
+// Device tables.  Where the per-call path itself cuts long rows into column
+// panels for the plan's N (B >= 64 MiB, at least kDevPanelMinPanels panels;
+// XL), the plan instead keeps that path's own tables: it runs plan_kernel and
+// the panel schedule once into a workspace of its own, and each call
+// launches only the main kernel, whose panel pieces interleave with the other
+// roles, and the combine pass.  Measured on MI355X for XL (Auto, N = 128):
+// 352 us per call through the derived CSR (its pieces launch ahead of the
+// rest, which the device-side schedule's single grid overlaps), against the
+// per-call path's 339 us; the tables are rebuilt when a call's N, column
+// width or alignment no longer matches them.
 
 #include <hip/hip_runtime.h>
 
@@ -88,6 +99,14 @@ struct csrspmm_plan_s {
   int* d_dcolidx = nullptr;
   float* d_dvals = nullptr;
   int* d_unit_start = nullptr;
+  // device tables (per-call path's tables, built once): the workspace and the
+  // N, column width and layout they were built for
+  bool dev_mode = false;
+  void* d_ws = nullptr;
+  size_t ws_bytes = 0;
+  int tab_n = 0, tab_vec = 0, tab_P = -1;
+  WorkspaceLayout tab_L{};
+  int dev_nl = 0;  // rows the device schedule panelized
   // partial buffers, grown with N
   long long ldp_cap = 0;
   float* d_partials = nullptr;
@@ -100,6 +119,7 @@ namespace {
 
 void plan_free(csrspmm_plan_s* p) {
   for (void* q : p->dev.ptrs) (void)hipFree(q);
+  if (p->d_ws) (void)hipFree(p->d_ws);
   if (p->d_partials) (void)hipFree(p->d_partials);
   if (p->d_pan_part) (void)hipFree(p->d_pan_part);
   delete p;
@@ -306,6 +326,66 @@ int build_rowgroup_plan(csrspmm_plan_s* p, const std::vector<int>& rp, int n_hin
   return to_status(e);
 }
 
+// Column panels the per-call path uses for N with this column width (0: none,
+// also when column slices take over).
+int device_panels(const csrspmm_plan_s* p, int vec, int N) {
+  const int P = per_call_panels(vec, true, p->K, N, p->nnz, p->maxlen);
+  return slice_width(p->K, N, P > 0) > 0 ? 0 : P;
+}
+
+// A Problem carrying the plan's CSR and tables for N (B and C are the call's).
+void bind_tables(const csrspmm_plan_s* p, Problem& q, int vec) {
+  q.plan = true;
+  bind_workspace(q, p->d_ws, p->tab_L, merge_block(vec, p->M, p->nnz));
+  set_row_hint(q, p->maxlen);
+}
+
+// Builds (or rebuilds) the per-call tables for N and column width vec into the
+// plan's workspace: plan_kernel and the panel schedule, on stream s.
+hipError_t build_device_tables(csrspmm_plan_s* p, int N, int vec, hipStream_t s) {
+  const int P = device_panels(p, vec, N);
+  const WorkspaceLayout L = workspace_layout(p->M, p->K, N, p->nnz, P);
+  hipError_t e = hipSuccess;
+  if (L.total > p->ws_bytes) {
+    e = hipStreamSynchronize(s);  // earlier calls may still use the old tables
+    if (e != hipSuccess) return e;
+    if (p->d_ws) (void)hipFree(p->d_ws);
+    p->d_ws = nullptr;
+    p->ws_bytes = 0;
+    e = hipMalloc(&p->d_ws, L.total);
+    if (e != hipSuccess) {
+      p->d_ws = nullptr;
+      return e;
+    }
+    p->ws_bytes = L.total;
+  }
+  p->tab_L = L;
+  p->tab_n = N;
+  p->tab_vec = vec;
+  p->tab_P = P;
+  Problem q{};
+  q.M = p->M;
+  q.K = p->K;
+  q.N = N;
+  q.nnz = p->nnz;
+  q.rowptr = p->rowptr;
+  q.colidx = p->colidx;
+  q.vals = p->vals;
+  const SegGeom g = seg_geom(p->nnz);
+  q.seg_shift = g.seg_shift;
+  q.slot_shift = g.slot_shift;
+  q.long_row = g.long_row;
+  bind_tables(p, q, vec);
+  e = launch_plan_tables(q, s);
+  if (e != hipSuccess) return e;
+  p->dev_nl = 0;
+  if (P > 0) {  // rows panelized (sched[0]), for csrspmm_plan_panelized_rows
+    e = hipMemcpyAsync(&p->dev_nl, q.dp.sched, sizeof(int), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+  }
+  return e;
+}
+
 }  // namespace
 
 extern "C" {
@@ -339,6 +419,20 @@ int csrspmm_plan_create(int algo, int M, int K, int nnz, const int* rowptr, cons
   if (is_rowgroup_algorithm(concrete)) {
     const int vec = (concrete == CSRSPMM_ALGO_WARP_PER_ROW_FP4 ||
                      concrete == CSRSPMM_ALGO_WARP_PER_ROW_SMEM_FP4) && n_eff % 4 == 0 ? 4 : 1;
+    int maxlen = 0;
+    for (int r = 0; r < M; ++r) maxlen = std::max(maxlen, rp[(size_t)r + 1] - rp[(size_t)r]);
+    p->maxlen = maxlen;
+    p->use_plan = ((long long)M + nnz >= kPlanMinItems) || maxlen > kSegLen;
+    p->dev_mode = p->use_plan && device_panels(p, vec, n_eff) > 0;
+    if (p->dev_mode) {
+      e = build_device_tables(p, n_eff, vec, static_cast<hipStream_t>(stream));
+      if (e != hipSuccess) {
+        plan_free(p);
+        return e == hipErrorOutOfMemory ? CSRSPMM_STATUS_ALLOC_FAILED : (int)e;
+      }
+      *out = p;
+      return 0;
+    }
     const int st = build_rowgroup_plan(p, rp, n_eff, vec);
     if (st != 0) {
       plan_free(p);
@@ -370,6 +464,23 @@ int csrspmm_plan_spmm_f32(csrspmm_plan_t plan, int N, const float* B, long long 
                         ldc, alpha, beta, flags);
   if (st != 0 || p->M == 0 || N == 0) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (p->dev_mode) {
+    // the per-call path with its tables built once: rebuilt when this call's
+    // panels, column width or partial width differ from theirs
+    const int vec = vector_width(p->algo, pr);
+    const int P = device_panels(p, vec, N);
+    const long long ldp = ((long long)N + 3) & ~3LL;
+    if (P != p->tab_P || vec != p->tab_vec || ldp > p->tab_L.ldp) {
+      const hipError_t eb = build_device_tables(p, N, vec, s);
+      if (eb != hipSuccess) return eb == hipErrorOutOfMemory ? CSRSPMM_STATUS_ALLOC_FAILED : (int)eb;
+    }
+    bind_tables(p, pr, vec);
+    pr.plan_ready = true;
+    pr.dp_ready = true;
+    pr.sw = P > 0 ? 0 : slice_width(p->K, N, false);
+    pr.slice_launch = slice_launches(p->M, p->nnz);
+    return to_status(launch_algorithm(p->algo, pr, s));
+  }
   hipError_t e = ensure_partials(p, N, s);
   if (e != hipSuccess) return CSRSPMM_STATUS_ALLOC_FAILED;
   pr.plan = true;
@@ -422,10 +533,13 @@ int csrspmm_plan_spmm_f32(csrspmm_plan_t plan, int N, const float* B, long long 
 int csrspmm_plan_algorithm(csrspmm_plan_t plan) { return plan ? plan->algo : -1; }
 
 size_t csrspmm_plan_device_bytes(csrspmm_plan_t plan) {
-  return plan ? plan->dev.bytes + plan->partial_bytes : 0;
+  return plan ? plan->dev.bytes + plan->partial_bytes + plan->ws_bytes : 0;
 }
 
-int csrspmm_plan_panelized_rows(csrspmm_plan_t plan) { return plan ? plan->npan : -1; }
+int csrspmm_plan_panelized_rows(csrspmm_plan_t plan) {
+  if (!plan) return -1;
+  return plan->dev_mode ? plan->dev_nl : plan->npan;
+}
 
 int csrspmm_plan_destroy(csrspmm_plan_t plan) {
   if (!plan) return 0;

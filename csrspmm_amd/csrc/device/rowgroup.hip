@@ -995,13 +995,20 @@ static hipError_t dispatch_vec1(const Problem& p, hipStream_t s) {
   return launch_rg<1, 64, 8, 4, LDS>(p, s);  // N > 512 loops over 512-column panels
 }
 
+hipError_t launch_plan_tables(const Problem& p, hipStream_t s) {
+  const int pblocks = std::min(div_up_host(p.M + 1, 256), 4096);
+  hipLaunchKernelGGL(plan_kernel, dim3(pblocks), dim3(256), 0, s, p);
+  if (p.dp.P > 0) return launch_panel_schedule(p, s);
+  return hipGetLastError();
+}
+
 static hipError_t launch_rowgroup_all(const Problem& p, int vec, bool lds, hipStream_t s) {
   if (p.plan && !p.plan_ready) {
     const int pblocks = std::min(div_up_host(p.M + 1, 256), 4096);
     hipLaunchKernelGGL(plan_kernel, dim3(pblocks), dim3(256), 0, s, p);
   }
   hipError_t e;
-  if (p.dp.P > 0) {
+  if (p.dp.P > 0 && !p.dp_ready) {
     e = launch_panel_schedule(p, s);
     if (e != hipSuccess) return e;
   }

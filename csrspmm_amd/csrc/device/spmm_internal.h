@@ -333,6 +333,9 @@ struct Problem {
   // are sorted and in range (plan_kernel sets it from rowptr,
   // panel_window_kernel clears it), else 0.
   unsigned char* dp_flag;
+  // A stored plan built the per-call panel schedule (dp) once: no panel
+  // schedule launches per call.
+  bool dp_ready;
 };
 
 // Segments of a row of len nonzeros under the problem's geometry and hint.
@@ -387,6 +390,10 @@ hipError_t launch_rowgroup(const Problem& p, int vec, bool lds, hipStream_t s);
 // and dp_flag, find the panel boundaries of the long rows, then compact the
 // panelized rows and deal the panels to the XCDs.
 hipError_t launch_panel_schedule(const Problem& p, hipStream_t s);
+
+// The tables of a planned call without the product: plan_kernel and, with
+// column panels, the panel schedule (stored plans build them once).
+hipError_t launch_plan_tables(const Problem& p, hipStream_t s);
 
 // Benchmark timing hook: no-ops unless csrspmm_timing_enable(1) was called.
 // Calls nest (per thread): only the outermost before/after pair records, so
