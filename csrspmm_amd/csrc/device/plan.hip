@@ -477,7 +477,9 @@ int csrspmm_plan_spmm_f32(csrspmm_plan_t plan, int N, const float* B, long long 
     bind_tables(p, pr, vec);
     pr.plan_ready = true;
     pr.dp_ready = true;
-    pr.sw = P > 0 ? 0 : slice_width(p->K, N, false);
+    pr.sw = P > 0 ? 0
+                  : slice_width(p->K, N, false,
+                                wide_sweep(vec, uses_lds(p->algo), true, p->M, p->K, p->nnz));
     pr.slice_launch = slice_launches(p->M, p->nnz);
     return to_status(launch_algorithm(p->algo, pr, s));
   }
@@ -494,15 +496,16 @@ int csrspmm_plan_spmm_f32(csrspmm_plan_t plan, int N, const float* B, long long 
   pr.partials = p->d_partials;
   pr.ldp = p->ldp_cap;
   pr.npan = p->npan;
+  const int vec = vector_width(p->algo, pr);
+  const bool lds = uses_lds(p->algo);
   // a plan with panelized rows keeps them; otherwise large B are sliced by columns
-  pr.sw = p->npan > 0 ? 0 : slice_width(p->K, N, false);
+  pr.sw = p->npan > 0 ? 0
+                      : slice_width(p->K, N, false, wide_sweep(vec, lds, true, p->M, p->K, p->nnz));
   pr.slice_launch = slice_launches(p->M, p->nnz);
   pr.pan_rows = p->d_pan_rows;
   pr.pan_ptr = p->d_pan_ptr;
   pr.pan_piece = p->d_pan_piece;
   pr.pan_part = p->d_pan_part;
-  const int vec = vector_width(p->algo, pr);
-  const bool lds = uses_lds(p->algo);
   timing_before_main(s);
   if (p->npan > 0) {
     // the pieces of panelized rows, alone first so nothing else evicts their band

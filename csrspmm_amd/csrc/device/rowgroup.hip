@@ -28,7 +28,10 @@
 //    short rows and stream their contiguous nonzeros, so gathers stay in
 //    flight across row boundaries and a row's accumulator is flushed
 //    (epilogue + store) when the stream passes its end.  With column slices
-//    the segment and merge blocks repeat per slice of columns.
+//    the segment and merge blocks repeat per slice of columns; float4
+//    slices of the register variant replace the merge blocks by a band
+//    sweep (sweep_rows), whose groups keep their rows for the whole slice
+//    and gather from B band after band.
 //  * combine_kernel: adds each split or panelized row's partials in a
 //    fixed order.
 // Everything is deterministic (no float atomics): results repeat bit for bit.
@@ -72,6 +75,15 @@ constexpr int kVec4U = CSRSPMM_VEC4_UNROLL;
 #define CSRSPMM_PIECES_PER_GROUP 1
 #endif
 constexpr int kPiecesPerGroup = CSRSPMM_PIECES_PER_GROUP;
+
+// Band sweep kernels: gathers in flight per lane in their long-row segments,
+// and the least waves per SIMD they are compiled for; build-time tunable.
+#ifndef CSRSPMM_SWEEP_SU
+#define CSRSPMM_SWEEP_SU 4
+#endif
+#ifndef CSRSPMM_SWEEP_WPE
+#define CSRSPMM_SWEEP_WPE 8
+#endif
 
 // B-row gathers in flight per lane in the pieces kernel; build-time tunable.
 #ifndef CSRSPMM_PIECE_UNROLL
@@ -333,6 +345,124 @@ __device__ __forceinline__ void stream_rows(const Problem& p, const Panel<VEC, G
   }
 }
 
+// Band sweep of the short rows of one column slice (float4, 16-lane groups,
+// B through a buffer resource).  The group owns rows [unit R, unit R + R)
+// and keeps their accumulators in registers through the whole slice.  All
+// groups start together and walk B in bands of 2^sweep_shift rows: in band
+// b each row takes its nonzeros whose columns fall in the band, so at any
+// time the running groups gather from about one band, which stays in the
+// L2s, instead of from all of B.  Column-sorted rows take their nonzeros in
+// CSR order band after band, so every row is summed in CSR order, as the
+// merge blocks sum it.  `bnd` (this group's LDS) first receives each row's
+// band starts: bnd[r][q] = the first nonzero whose column lies in band q or
+// later (the row end when there is none), from one pass over the row's
+// columns.  A row with a column out of order or out of range takes all its
+// nonzeros in band 0, in CSR order.  A row longer than long_row is skipped
+// (its segments are summed elsewhere) unless the rows are summed whole.
+template <int R>
+__device__ __forceinline__ void sweep_rows(const Problem& p, const Panel<4, 16, 1, true>& pn, int unit,
+                                           int gl, int gbase, int* bnd) {
+  constexpr int G = 16;
+  constexpr int NB1 = kSweepMaxBands + 1;
+  const unsigned long long gmask = 0xFFFFull << gbase;
+  const int nb = p.sweep_bands;
+  const int sh = p.sweep_shift;
+  bool keep[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int row = unit * R + r;
+    int lo = 0, hi = 0;
+    if (row < p.M) {
+      lo = p.rowptr[row];
+      hi = p.rowptr[row + 1];
+    }
+    keep[r] = row < p.M && (p.rows_whole || hi - lo <= p.long_row);
+    const int x0 = clamp_nnz(lo, p.nnz);
+    const int x1 = keep[r] ? max(clamp_nnz(hi, p.nnz), x0) : x0;
+    int* bd = bnd + r * NB1;
+    // positions x0 .. x1 (x1 closes the row as band nb); the previous
+    // position's band is lane gl - 1's (lane 0: the carry)
+    int carry = -1;
+    bool bad = false;
+    for (int c = x0; c <= x1; c += G) {
+      const int j = c + gl;
+      int q = nb;
+      if (j < x1) {
+        const int col = ld_stream(p.colidx + j);
+        bad |= col < 0 || col >= p.K;
+        q = min(max(col, 0) >> sh, nb - 1);
+      }
+      int qp = group_bcast<G>(q, gbase, (gl + G - 1) & (G - 1));
+      const int ql = group_bcast<G>(q, gbase, G - 1);
+      if (gl == 0) qp = carry;
+      carry = ql;
+      if (j <= x1) {
+        bad |= qp > q;
+        for (int t = qp + 1; t <= q; ++t) bd[t] = j;
+      }
+    }
+    if (__ballot(bad) & gmask) {
+      wave_lds_sync();
+      for (int t = gl; t <= nb; t += G) bd[t] = t == 0 ? x0 : x1;
+    }
+  }
+  wave_lds_sync();
+
+  f4 acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = Vec<4>::zero();
+  for (int b = 0; b < nb; ++b) {
+    int s[R], cnt[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      s[r] = bnd[r * NB1 + b];
+      cnt[r] = bnd[r * NB1 + b + 1] - s[r];
+    }
+    for (int base = 0;; base += G) {
+      bool more = false;
+#pragma unroll
+      for (int r = 0; r < R; ++r) more |= base < cnt[r];
+      if (!__any(more)) break;
+      int cj[R];
+      float vj[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const bool in = base + gl < cnt[r];
+        cj[r] = in ? ld_stream(p.colidx + s[r] + base + gl) : 0;
+        vj[r] = in ? ld_stream(p.vals + s[r] + base + gl) : 0.0f;
+      }
+      // One gather per row in flight at a time: measured on MI355X (65536 x
+      // 65536 x 256, 66 per row), 2 rows x 1 ran 286 us, 2 x 2 427 us, 1 x 2
+      // 310 us, 1 x 4 477 us.  An entry past a row's count gets an offset
+      // past the buffer (nothing fetched) and a value of 0, which leaves the
+      // accumulator as it is.
+      for (int k = 0; k < G; ++k) {
+        bool any = false;
+#pragma unroll
+        for (int r = 0; r < R; ++r) any |= base + k < cnt[r];
+        if (!__any(any)) break;
+        f4 bv[R];
+        float v[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const int c = group_bcast<G>(cj[r], gbase, k);
+          v[r] = group_bcast<G>(vj[r], gbase, k);
+          const unsigned off =
+              base + k < cnt[r] ? __umul24((unsigned)c, pn.bb.rowbytes) + pn.colbytes[0] : kBufOffPast;
+          bv[r] = ld_b_buf<4>(pn.bb, off);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = fma_v(v[r], bv[r], acc[r]);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    f4 a[1] = {acc[r]};
+    if (keep[r]) store_row<4, 1>(p, unit * R + r, pn.col, pn.cval, a);
+  }
+}
+
 // Pieces of this call's column panels, run by the first blocks of the main
 // launch.  Pieces block b takes chunk b / kXcds of XCD b mod kXcds's piece
 // list: kPiecesPerGroup * GPB consecutive pieces, group g taking pieces
@@ -429,9 +559,10 @@ __device__ __forceinline__ void pieces_body(const Problem& p, int block, int gl,
 // One block's share of the main launch, over the columns [c_lo, c_hi):
 // block bid < seg_blocks takes long-row segment slots, the others merge
 // blocks of short rows (or, without a plan, rows).
-template <int VEC, int G, int T, int U, bool LDS, bool BUF, int SU>
+template <int VEC, int G, int T, int U, bool LDS, bool BUF, int SU, bool SWEEP>
 __device__ __forceinline__ void rowgroup_block(const Problem& p, int bid, int seg_blocks, int c_lo,
-                                               int c_hi, int gl, int gbase, int gid, int2* stage) {
+                                               int c_hi, int gl, int gbase, int gid, int2* stage,
+                                               int* sweep_bnd) {
   using VT = typename Vec<VEC>::T;
   constexpr int GPB = kWaves * (64 / G);
   constexpr int PW = G * VEC * T;
@@ -476,6 +607,13 @@ __device__ __forceinline__ void rowgroup_block(const Problem& p, int bid, int se
   }
 
   const int unit = (bid - seg_blocks) * GPB + gid;
+  if constexpr (SWEEP) {
+    // The band sweep of a column slice: kSweepRows rows per group.
+    static_assert(VEC == 4 && G == 16 && T == 1 && BUF, "the sweep runs 64-column float4 slices");
+    const Panel<VEC, G, T, BUF> pn(p, c_lo, gl, c_hi);
+    sweep_rows<kSweepRows>(p, pn, unit, gl, gbase, sweep_bnd + gid * kSweepRows * (kSweepMaxBands + 1));
+    return;
+  }
   if (p.plan) {
     // One merge block of short rows.
     if (unit >= p.nblocks) return;
@@ -558,8 +696,8 @@ __device__ __forceinline__ void interleave_roles(int b, int piece_blocks, int to
 // column panels).  The kernels of calls without them are compiled without
 // that code, which as dead code cost the scalar N <= 64 kernel 9% on R-MAT
 // and the scalar N = 128 / 256 kernels 3-18% on the reference's sweep shapes.
-template <int VEC, int G, int T, int U, bool LDS, bool PIECES, int SU, bool BUF>
-__global__ __launch_bounds__(kWaves * 64) void rowgroup_kernel(Problem p, int piece_blocks,
+template <int VEC, int G, int T, int U, bool LDS, bool PIECES, int SU, bool BUF, bool SWEEP>
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(SWEEP ? CSRSPMM_SWEEP_WPE : 1))) void rowgroup_kernel(Problem p, int piece_blocks,
                                                                 int seg_blocks, int slice_blocks,
                                                                 int slice0) {
   constexpr int GPW = 64 / G;  // groups per wave
@@ -571,6 +709,8 @@ __global__ __launch_bounds__(kWaves * 64) void rowgroup_kernel(Problem p, int pi
 
   __shared__ int2 stage_all[LDS ? kWaves * 64 : 1];
   int2* stage = stage_all + (LDS ? wave * 64 : 0);
+  // band starts of the sweep's rows, kSweepRows x (kSweepMaxBands + 1) per group
+  __shared__ int sweep_bnd[SWEEP ? kWaves * GPW * kSweepRows * (kSweepMaxBands + 1) : 1];
 
   int bid = (int)blockIdx.x - piece_blocks;
   if constexpr (PIECES) {
@@ -594,7 +734,8 @@ __global__ __launch_bounds__(kWaves * 64) void rowgroup_kernel(Problem p, int pi
     c_lo = (slice0 + local) * p.sw;
     c_hi = min(p.N, c_lo + p.sw);
   }
-  rowgroup_block<VEC, G, T, U, LDS, BUF, SU>(p, bid, seg_blocks, c_lo, c_hi, gl, gbase, gid, stage);
+  rowgroup_block<VEC, G, T, U, LDS, BUF, SU, SWEEP>(p, bid, seg_blocks, c_lo, c_hi, gl, gbase, gid, stage,
+                                                     sweep_bnd);
 }
 
 // Table entries of one row r: the merge-block starts [b_lo, b_hi], the
@@ -869,10 +1010,12 @@ void launch_combine(const Problem& p, hipStream_t s) {
 
 // SU: B-row gathers in flight per lane in the long-row segments (at least U).
 // BUF: B gathered through a buffer resource (buf_gathers_ok must hold).
-template <int VEC, int G, int T, int U, bool LDS, int SU = CSRSPMM_SEG_UNROLL, bool BUF = false>
+// SWEEP: the short rows of each slice in a band sweep (p.sweep_bands > 0).
+template <int VEC, int G, int T, int U, bool LDS, int SU = CSRSPMM_SEG_UNROLL, bool BUF = false,
+          bool SWEEP = false>
 hipError_t launch_rg(const Problem& p, hipStream_t s) {
   constexpr int GPB = kWaves * (64 / G);
-  const int units = p.plan ? p.nblocks : p.M;
+  const int units = SWEEP ? div_up_host(p.M, kSweepRows) : p.plan ? p.nblocks : p.M;
   const int unit_blocks = div_up_host(units, GPB);
   const int seg_blocks =
       (p.plan && p.nslots > 0) ? std::min(kSegBlocksMax, div_up_host(p.nslots, GPB)) : 0;
@@ -895,7 +1038,7 @@ hipError_t launch_rg(const Problem& p, hipStream_t s) {
   const int per_launch = (p.sw > 0 && p.slice_launch) ? 1 : nslices;
   // Unused LDS that leaves room for only `cap` blocks per CU (a multiple of
   // 512 bytes, the allocation unit, per block with the static stage).
-  const int cap = slice_blocks_per_cu(p.K, p.sw, p.slice_launch);
+  const int cap = SWEEP ? 0 : slice_blocks_per_cu(p.K, p.sw, p.slice_launch);
   constexpr int kStaticLds = (LDS ? kWaves * 64 : 1) * (int)sizeof(int2);
   const int pad_lds = cap > 0 ? (kLdsPerCu / cap) / 512 * 512 - kStaticLds : 0;
   for (int s0 = 0; s0 < nslices; s0 += per_launch) {
@@ -903,11 +1046,11 @@ hipError_t launch_rg(const Problem& p, hipStream_t s) {
     if (blocks == 0) return hipSuccess;
     if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
     if (piece_blocks > 0) {
-      hipLaunchKernelGGL((rowgroup_kernel<VEC, G, T, U, LDS, kCanPanel, SU, BUF>), dim3((unsigned)blocks),
+      hipLaunchKernelGGL((rowgroup_kernel<VEC, G, T, U, LDS, kCanPanel, SU, BUF, false>), dim3((unsigned)blocks),
                          dim3(kWaves * 64), pad_lds, s, p, piece_blocks, seg_blocks, slice_blocks,
                          s0);
     } else {
-      hipLaunchKernelGGL((rowgroup_kernel<VEC, G, T, U, LDS, false, SU, BUF>), dim3((unsigned)blocks),
+      hipLaunchKernelGGL((rowgroup_kernel<VEC, G, T, U, LDS, false, SU, BUF, SWEEP>), dim3((unsigned)blocks),
                          dim3(kWaves * 64), pad_lds, s, p, 0, seg_blocks, slice_blocks, s0);
     }
   }
@@ -971,7 +1114,16 @@ static hipError_t dispatch_vec4(const Problem& p, hipStream_t s) {
   // 276 us, K = 65536 325 -> 304; the 66-per-row uniform and R-MAT N = 512
   // configs within 1%.  Unsliced 16-lane calls keep 4 (XL at N = 64 lost 7%).
   static_assert(kSliceWidth == 64, "a slice's float4 chunks fill 16-lane groups");
-  if (p.sw == kSliceWidth) return launch_rg<4, 16, 1, kVec4U, LDS, 8>(p, s);
+  if (p.sw == kSliceWidth) {
+    // The register variant sweeps the short rows of each slice band by band
+    // (sweep_rows); the LDS-staged variant keeps the merge blocks.
+    if (!LDS && sweep_applies(p.plan, p.M, p.K, p.nnz, p.sw) && buf_gathers_ok(p)) {
+      Problem q = p;
+      sweep_geometry(p.K, p.sw, q.sweep_shift, q.sweep_bands);
+      return launch_rg<4, 16, 1, kVec4U, false, CSRSPMM_SWEEP_SU, true, true>(q, s);
+    }
+    return launch_rg<4, 16, 1, kVec4U, LDS, 8>(p, s);
+  }
   if (buf_gathers_ok(p)) return dispatch_vec4_cols<LDS, true>(p, s);
   return dispatch_vec4_cols<LDS, false>(p, s);
 }

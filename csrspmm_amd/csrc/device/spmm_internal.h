@@ -207,12 +207,28 @@ inline bool slice_launches(int M, int nnz) {
 #ifndef CSRSPMM_SLICE_MIN_MB
 #define CSRSPMM_SLICE_MIN_MB 32
 #endif
-inline int slice_width(int K, int N, bool panels) {
+#ifndef CSRSPMM_SLICE_BAND_MAX_MB
+#define CSRSPMM_SLICE_BAND_MAX_MB 16
+#endif
+// `sweeps`: the call would sweep its slices with rows averaging at least
+// kSweepWideMinPerBand nonzeros per band (wide_sweep); with no column panels
+// possible (a max_row_nnz hint below kPanelMinLen, or a stored plan without
+// such rows), such a call slices bands of any width.  Measured on MI355X with
+// the hint, against no slices: 131072 x 131072 x 256 with 66 per row
+// 1208 -> 875 us, 32 per row 600 -> 546 us; 98304^2 x 256 with 48 per row
+// 663 -> 444 us; 262144^2 x 256 with 32 per row (2 per band) 1222 -> 1409
+// us, below the threshold.
+#ifndef CSRSPMM_SWEEP_WIDE
+#define CSRSPMM_SWEEP_WIDE 1
+#endif
+constexpr int kSweepWideMinPerBand = 4;
+inline int slice_width(int K, int N, bool panels, bool sweeps = false) {
   const long long full = (long long)K * N * 4;
   const long long band = (long long)K * kSliceWidth * 4;
   if (N < 2 * kSliceWidth || full < ((long long)CSRSPMM_SLICE_MIN_MB << 20)) return 0;
   if (N <= 128 && panels) return 0;
-  if (band > (16LL << 20) && full < (1LL << 30)) return 0;
+  const bool wide = CSRSPMM_SWEEP_WIDE && sweeps && !panels;
+  if (band > ((long long)CSRSPMM_SLICE_BAND_MAX_MB << 20) && full < (1LL << 30) && !wide) return 0;
   return kSliceWidth;
 }
 
@@ -336,7 +352,53 @@ struct Problem {
   // A stored plan built the per-call panel schedule (dp) once: no panel
   // schedule launches per call.
   bool dp_ready;
+  // Band sweep of the short rows of a column slice (sweep_geometry; bands 0:
+  // merge blocks instead): bands of 2^sweep_shift B rows, sweep_bands of them.
+  int sweep_shift, sweep_bands;
 };
+
+// Band sweep (sliced float4 calls).  Each group keeps kSweepRows rows'
+// accumulators in registers while all groups walk the slice's band of B in
+// bands of about kSweepBandBytes, so a band stays in the L2s while every row
+// takes its nonzeros in it.  Measured on MI355X, per call against the merge
+// blocks (bit-identical): 65536 x 65536 x 256 with 66 per row 387 -> 286 us
+// (L2 hit rate per slice 0.47 -> 0.70, fetched bytes -42%), 16 per row
+// 151 -> 113 us, 128 per row 870 -> 460 us; 131072 x 131072 x 256 with 66
+// per row 1247 -> 806 us; 65536 x 65536 x 512 with 66 per row 765 -> 572 us.
+#ifndef CSRSPMM_SWEEP_BAND_KB
+#define CSRSPMM_SWEEP_BAND_KB 4096
+#endif
+constexpr int kSweepRows = 2;
+constexpr int kSweepMaxBands = 64;
+// (shift, bands) for a K-row B swept in slices of sw columns: the smallest
+// power-of-two band of at least CSRSPMM_SWEEP_BAND_KB KiB, widened until
+// at most kSweepMaxBands cover K.
+inline void sweep_geometry(int K, int sw, int& shift, int& bands) {
+  shift = 0;
+  while (((long long)sw * 4 << shift) < ((long long)CSRSPMM_SWEEP_BAND_KB << 10)) ++shift;
+  while (((long long)K + (1LL << shift) - 1) >> shift > kSweepMaxBands) ++shift;
+  bands = (int)(((long long)K + (1LL << shift) - 1) >> shift);
+}
+// The sweep pays when rows average enough nonzeros per band.  Measured on
+// MI355X: 65536 x 65536 x 256 with 8 per row (2 per band) 88.7 -> 79.2 us,
+// with 16 per row (4 per band) 148.5 -> 119.9 us; R-MAT N = 512 (15 per row,
+// 0.24 per band) 4.86 -> 9.03 ms, so it keeps the merge blocks.
+#ifndef CSRSPMM_SWEEP_MIN_PER_BAND
+#define CSRSPMM_SWEEP_MIN_PER_BAND 2
+#endif
+inline bool sweep_applies(bool plan, int M, int K, int nnz, int sw,
+                          int min_per_band = CSRSPMM_SWEEP_MIN_PER_BAND) {
+  if (!plan || sw <= 0 || M <= 0 || K <= 0) return false;
+  int shift, bands;
+  sweep_geometry(K, sw, shift, bands);
+  return (long long)nnz >= (long long)min_per_band * bands * M;
+}
+// The call's slices would be swept (float4 columns, vec 4, of the register
+// variant, with a plan) with at least kSweepWideMinPerBand nonzeros per band
+// and row: slice_width's `sweeps`.
+inline bool wide_sweep(int vec, bool lds, bool plan, int M, int K, int nnz) {
+  return vec == 4 && !lds && sweep_applies(plan, M, K, nnz, kSliceWidth, kSweepWideMinPerBand);
+}
 
 // Segments of a row of len nonzeros under the problem's geometry and hint.
 __host__ __device__ inline int seg_count(const Problem& p, int len) {
