@@ -411,13 +411,22 @@ __device__ __forceinline__ void sweep_rows(const Problem& p, const Panel<4, 16, 
   f4 acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = Vec<4>::zero();
-  for (int b = 0; b < nb; ++b) {
-    int s[R], cnt[R];
+  // (col, val) of lane gl's entry of band b's chunk at `base` for every row
+  auto load_chunk_rows = [&](int b, int base, int (&c)[R], float (&v)[R]) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      s[r] = bnd[r * NB1 + b];
-      cnt[r] = bnd[r * NB1 + b + 1] - s[r];
+      const int s0 = bnd[r * NB1 + b];
+      const bool in = base + gl < bnd[r * NB1 + b + 1] - s0;
+      c[r] = in ? ld_stream(p.colidx + s0 + base + gl) : 0;
+      v[r] = in ? ld_stream(p.vals + s0 + base + gl) : 0.0f;
     }
+  };
+  // (A prefetch of the next band's first chunk during this band's gathers
+  // measured 1-3% slower on MI355X.)
+  for (int b = 0; b < nb; ++b) {
+    int cnt[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) cnt[r] = bnd[r * NB1 + b + 1] - bnd[r * NB1 + b];
     for (int base = 0;; base += G) {
       bool more = false;
 #pragma unroll
@@ -425,12 +434,7 @@ __device__ __forceinline__ void sweep_rows(const Problem& p, const Panel<4, 16, 
       if (!__any(more)) break;
       int cj[R];
       float vj[R];
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const bool in = base + gl < cnt[r];
-        cj[r] = in ? ld_stream(p.colidx + s[r] + base + gl) : 0;
-        vj[r] = in ? ld_stream(p.vals + s[r] + base + gl) : 0.0f;
-      }
+      load_chunk_rows(b, base, cj, vj);
       // One gather per row in flight at a time: measured on MI355X (65536 x
       // 65536 x 256, 66 per row), 2 rows x 1 ran 286 us, 2 x 2 427 us, 1 x 2
       // 310 us, 1 x 4 477 us.  An entry past a row's count gets an offset
