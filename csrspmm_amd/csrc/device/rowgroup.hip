@@ -1132,23 +1132,37 @@ static hipError_t dispatch_vec4(const Problem& p, hipStream_t s) {
   return dispatch_vec4_cols<LDS, false>(p, s);
 }
 
-template <bool LDS>
-static hipError_t dispatch_vec1(const Problem& p, hipStream_t s) {
+template <bool LDS, bool BUF>
+static hipError_t dispatch_vec1_cols(const Problem& p, hipStream_t s) {
+  constexpr int SU = CSRSPMM_SEG_UNROLL;
   const int n = p.sw > 0 ? std::min(p.sw, p.N) : p.N;
   const int G = n >= 64 ? 64 : (pow2_ceil(n) < 4 ? 4 : pow2_ceil(n));
   if (G < 64) {
     switch (G) {
-      case 4: return launch_rg<1, 4, 1, 8, LDS>(p, s);
-      case 8: return launch_rg<1, 8, 1, 8, LDS>(p, s);
-      case 16: return launch_rg<1, 16, 1, 8, LDS>(p, s);
-      default: return launch_rg<1, 32, 1, 8, LDS>(p, s);
+      case 4: return launch_rg<1, 4, 1, 8, LDS, SU, BUF>(p, s);
+      case 8: return launch_rg<1, 8, 1, 8, LDS, SU, BUF>(p, s);
+      case 16: return launch_rg<1, 16, 1, 8, LDS, SU, BUF>(p, s);
+      default: return launch_rg<1, 32, 1, 8, LDS, SU, BUF>(p, s);
     }
   }
   const int t = (n + 63) / 64;
-  if (t <= 1) return launch_rg<1, 64, 1, 8, LDS>(p, s);
-  if (t <= 2) return launch_rg<1, 64, 2, 8, LDS>(p, s);
-  if (t <= 4) return launch_rg<1, 64, 4, 8, LDS>(p, s);
-  return launch_rg<1, 64, 8, 4, LDS>(p, s);  // N > 512 loops over 512-column panels
+  if (t <= 1) return launch_rg<1, 64, 1, 8, LDS, SU, BUF>(p, s);
+  if (t <= 2) return launch_rg<1, 64, 2, 8, LDS, SU, BUF>(p, s);
+  if (t <= 4) return launch_rg<1, 64, 4, 8, LDS, SU, BUF>(p, s);
+  return launch_rg<1, 64, 8, 4, LDS, SU, BUF>(p, s);  // N > 512 loops over 512-column panels
+}
+
+// Scalar-column calls gather B through a buffer resource when it fits
+// (buf_gathers_ok), sliced or not.  Measured on MI355X against 64-bit global
+// loads, per call, bit-identical: XL WarpPerRow 510 -> 394 us and
+// WarpPerRowSmem 416 -> 357; medium WarpPerRow 84 -> 59 and WarpPerRowSmem
+// 67 -> 59; R-MAT N = 32 (Auto) 388 -> 307; sliced, large WarpPerRow 690 ->
+// 535 and WarpPerRowSmem 575 -> 525, R-MAT N = 512 WarpPerRow 5122 -> 4753;
+// R-MAT N = 64 (Auto) within 0.6%.
+template <bool LDS>
+static hipError_t dispatch_vec1(const Problem& p, hipStream_t s) {
+  if (buf_gathers_ok(p)) return dispatch_vec1_cols<LDS, true>(p, s);
+  return dispatch_vec1_cols<LDS, false>(p, s);
 }
 
 hipError_t launch_plan_tables(const Problem& p, hipStream_t s) {
