@@ -111,7 +111,11 @@ int csrspmm_workspace_panel_info(int algo, int M, int K, int N, int nnz, int max
  * torch forwards' launch (reference torch_csrspmm/torch_csrspmm_*.cpp).
  *   algo            CSRSPMM_ALGO_*
  *   M, K, N, nnz    A is M x K with nnz nonzeros; B is K x N; C is M x N
- *   rowptr, colidx, vals   device CSR arrays (M+1, nnz, nnz entries)
+ *   rowptr, colidx, vals   device CSR arrays (M+1, nnz, nnz entries); as in
+ *                   the reference, rowptr must run from 0 to nnz without
+ *                   decreasing and every column must lie in [0, K); the
+ *                   per-call path does not check (csrspmm_validate_csr does).
+ *                   Columns need not be sorted within a row.
  *   max_row_nnz_hint       -1 if unknown; otherwise the caller's claim of the
  *                   longest row.  It only steers the plan: at most 128 drops
  *                   the long-row segments and their combine pass, below 512
