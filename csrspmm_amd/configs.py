@@ -32,6 +32,10 @@ class Config:
             return gen.rmat(p["scale"], p["samples"], p["a"], p["b"], p["c"], self.seed)
         raise ValueError(self.kind)
 
+    def K(self) -> int:
+        """Columns of A (rows of B), without generating the matrix."""
+        return 1 << self.params["scale"] if self.kind == "rmat" else self.params["K"]
+
     def B(self, K: int):
         return gen.dense(self.seed, gen.TAG_B, K, self.N)
 

@@ -219,6 +219,21 @@ int owned_workspace_locked(void* stream, size_t bytes, void** out) {
 
 }  // namespace
 
+int resolve_algorithm(int algo, int M, int K, int N, int nnz) {
+  if (algo == CSRSPMM_ALGO_AUTO && N % 4 == 0 && N == 128 && M >= 4096 &&
+      (long long)K * N * 4 <= (4LL << 20) && (long long)nnz >= 160LL * M) {
+    // A B that stays in the L2s and rows of 160 nonzeros or more on average:
+    // the rows are long-row segments, and the scalar LDS-staged form keeps
+    // more gathers in flight per row.  Measured on MI355X per call, uniform
+    // rows at N = 128 with max_row_nnz given: M = 4096, K = 4096, 205 per row
+    // 33.2 -> 23.0 us, 600 per row 81.8 -> 66.8; M = 16384, K = 2048, 205
+    // per row 90.7 -> 68.8; but 64 per row, M = 1024, an 8 MiB B (K = 16384)
+    // or N = 256 keep float4 within 0-21%.
+    return CSRSPMM_ALGO_WARP_PER_ROW_SMEM;
+  }
+  return resolve_algorithm(algo, N);
+}
+
 int resolve_algorithm(int algo, int N) {
   if (algo == CSRSPMM_ALGO_AUTO) {
     // Measured on MI355X: float4 columns win from N = 128 up, scalar columns
@@ -336,7 +351,7 @@ int spmm_impl(int algo_in, int M, int K, int N, int nnz, const int* rowptr, cons
               const float* vals, int hint, const float* B, long long ldb, float* C, long long ldc,
               float alpha, float beta, unsigned flags, void* ws, size_t ws_bytes, bool owned,
               void* stream) {
-  const int algo = resolve_algorithm(algo_in, N);
+  const int algo = resolve_algorithm(algo_in, M, K, N, nnz);
   Problem p;
   int st = fill_problem(p, algo, M, K, N, nnz, rowptr, colidx, vals, B, ldb, C, ldc, alpha, beta, flags);
   if (st != 0) return st;
@@ -506,6 +521,9 @@ const char* csrspmm_algorithm_name(int algo) {
 }
 
 int csrspmm_resolve_algorithm(int algo, int N) { return resolve_algorithm(algo, N); }
+int csrspmm_resolve_algorithm_ex(int algo, int M, int K, int N, int nnz) {
+  return resolve_algorithm(algo, M, K, N, nnz);
+}
 
 size_t csrspmm_workspace_bytes(int algo, int M, int N, int nnz) {
   algo = resolve_algorithm(algo, N);
@@ -516,7 +534,7 @@ size_t csrspmm_workspace_bytes(int algo, int M, int N, int nnz) {
 // The panels of a per-call product as far as the shape tells (pointer
 // alignment is checked per call); -1 when the call makes no plan.
 static int shape_panels(int algo, int M, int K, int N, int nnz, int hint) {
-  algo = resolve_algorithm(algo, N);
+  algo = resolve_algorithm(algo, M, K, N, nnz);
   if (M <= 0 || N <= 0 || nnz < 0 || K < 0 || !wants_plan(algo, M, nnz, hint)) return -1;
   const bool fp4 = (algo == CSRSPMM_ALGO_WARP_PER_ROW_FP4 || algo == CSRSPMM_ALGO_WARP_PER_ROW_SMEM_FP4) &&
                    N % 4 == 0;

@@ -398,7 +398,7 @@ int csrspmm_plan_create(int algo, int M, int K, int nnz, const int* rowptr, cons
     return CSRSPMM_STATUS_INVALID_VALUE;
   if ((long long)M + nnz + 1 > 0x7fffffffLL - kMergeBlockMax) return CSRSPMM_STATUS_NOT_SUPPORTED;
   const int n_eff = n_hint > 0 ? n_hint : 128;
-  const int concrete = resolve_algorithm(algo, n_eff);
+  const int concrete = resolve_algorithm(algo, M, K, n_eff, nnz);
   if (concrete < 0) return CSRSPMM_STATUS_INVALID_VALUE;
   hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));  // A must be ready
   if (e != hipSuccess) return (int)e;

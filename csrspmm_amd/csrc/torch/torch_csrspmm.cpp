@@ -326,7 +326,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("dense_to_csr", &dense_to_csr, "device dense -> CSR (rowptr, colidx, values)");
   m.def("csr_max_row_nnz", &csr_max_row_nnz, "longest row, on the device");
   m.def("indices_to_int32", &indices_to_int32, "int64 -> int32 CSR indices, on the device");
-  m.def("csrspmm_auto", &csrspmm_auto_forward, "CSR SpMM (variant picked from N)");
+  m.def("csrspmm_auto", &csrspmm_auto_forward, "CSR SpMM (variant picked from the shape)");
   m.def("csrspmm_spmm_out", &csrspmm_spmm_out, "CSR SpMM into C in place (C = alpha*A*B + beta*C)");
   pybind11::class_<CsrSpmmPlan>(m, "CsrSpmmPlan")
       .def(pybind11::init<Tensor, Tensor, Tensor, int64_t, const std::string&, int64_t>())

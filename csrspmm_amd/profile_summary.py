@@ -109,8 +109,8 @@ def summarize(prof: str, name: str):
     from . import capi
 
     lib = capi.hip()
-    resolved = lib.csrspmm_algorithm_name(
-        lib.csrspmm_resolve_algorithm(capi.ALGO[info["algo"]], info["N"])).decode()
+    resolved = lib.csrspmm_algorithm_name(lib.csrspmm_resolve_algorithm_ex(
+        capi.ALGO[info["algo"]], info["M"], cfg.K(), info["N"], info["nnz"])).decode()
     what = {"plan": "stored plan, ", "nopanels": "no column panels (base-size workspace), "}.get(
         info["mode"], "")
     lines = [

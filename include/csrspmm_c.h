@@ -77,9 +77,16 @@ int csrspmm_parse_algorithm(const char* name);
 /* Algorithm id -> CamelCase name ("Auto" for CSRSPMM_ALGO_AUTO), or NULL. */
 const char* csrspmm_algorithm_name(int algo);
 
-/* The concrete variant CSRSPMM_ALGO_AUTO runs for N output columns (a
- * concrete id is returned unchanged; -1 for an invalid id). */
+/* The concrete variant CSRSPMM_ALGO_AUTO picks from N output columns alone
+ * (a concrete id is returned unchanged; -1 for an invalid id). */
 int csrspmm_resolve_algorithm(int algo, int N);
+/* The concrete variant CSRSPMM_ALGO_AUTO runs for the whole shape (A is
+ * M x K with nnz nonzeros, N output columns): csrspmm_resolve_algorithm's
+ * choice, except that at N = 128 a B of at most 4 MiB with rows of 160 or
+ * more nonzeros on average (M >= 4096) takes the scalar LDS-staged variant.
+ * The SpMM entry points and stored plans resolve Auto this way.  No
+ * counterpart in the reference, whose Auto stub is empty. */
+int csrspmm_resolve_algorithm_ex(int algo, int M, int K, int N, int nnz);
 
 /* Bytes of device workspace csrspmm_spmm_f32_ws needs for this problem
  * (row-split plan, partial sums of split rows, counters).  No counterpart in

@@ -50,6 +50,19 @@ def test_parse_and_names():
     assert lib.csrspmm_resolve_algorithm(6, 130) == 4
     assert lib.csrspmm_resolve_algorithm(2, 128) == 2
     assert lib.csrspmm_resolve_algorithm(9, 128) == -1
+    # From the whole shape: at N = 128 an L2-sized B (<= 4 MiB) with long rows
+    # (>= 160 per row on average, M >= 4096) takes WarpPerRowSmem
+    ex = lib.csrspmm_resolve_algorithm_ex
+    assert ex(6, 4096, 4096, 128, 4096 * 160) == 4
+    assert ex(6, 4096, 8192, 128, 4096 * 160) == 4          # B exactly 4 MiB
+    assert ex(6, 4096, 8193, 128, 4096 * 160) == 3          # B above 4 MiB
+    assert ex(6, 4096, 4096, 128, 4096 * 160 - 1) == 3      # rows shorter
+    assert ex(6, 4095, 4096, 128, 4095 * 200) == 3          # fewer rows
+    assert ex(6, 4096, 4096, 256, 4096 * 200) == 3          # N = 256
+    assert ex(6, 4096, 4096, 64, 4096 * 200) == 4           # below 128: scalar anyway
+    assert ex(6, 262144, 262144, 128, 8453223) == 3         # XL
+    assert ex(3, 4096, 4096, 128, 4096 * 200) == 3          # concrete ids pass through
+    assert ex(9, 4096, 4096, 128, 4096 * 200) == -1
     assert lib.csrspmm_version() >= 100
 
 

@@ -108,3 +108,28 @@ def test_auto_per_call(cfg_name, gpu):
     algo = capi.hip().csrspmm_algorithm_name(capi.hip().csrspmm_resolve_algorithm(6, cfg.N)).decode()
     assert_parity(algo, C, a.rowptr, a.colidx, a.vals, B, None, 1.0, 0.0, rows=sample_rows(a, False),
                   what="auto")
+
+
+def test_auto_takes_scalar_lds_on_l2_sized_long_rows(gpu):
+    """At N = 128 a B of at most 4 MiB with rows of 160 nonzeros or more on
+    average (M >= 4096) resolves Auto to WarpPerRowSmem, per call and in a
+    stored plan: bit-identical to that variant and within the oracle's bar."""
+    from csrspmm_amd import gen
+    M, K, N = 4096, 4096, 128
+    a = gen.uniform(M, K, 200, 21)
+    B = gen.dense(21, gen.TAG_B, K, N)
+    ex = capi.hip().csrspmm_resolve_algorithm_ex(capi.ALGO["Auto"], M, K, N, a.nnz)
+    assert capi.hip().csrspmm_algorithm_name(ex).decode() == "WarpPerRowSmem"
+    from test_gpu_parity import run_spmm
+    C_auto = run_spmm("Auto", a.rowptr, a.colidx, a.vals, B, gpu)
+    C_smem = run_spmm("WarpPerRowSmem", a.rowptr, a.colidx, a.vals, B, gpu)
+    assert np.array_equal(C_auto, C_smem)
+    assert_parity("WarpPerRowSmem", C_auto, a.rowptr, a.colidx, a.vals, B, None, 1.0, 0.0,
+                  rows=np.arange(0, M, 7), what="auto shape rule")
+    rp, ci, va = dev_t(a.rowptr, gpu), dev_t(a.colidx, gpu), dev_t(a.vals, gpu)
+    plan = capi.Plan("Auto", rp, ci, va, K, n_hint=N)
+    assert plan.algorithm == "WarpPerRowSmem"
+    C_plan = plan_run(plan, B, gpu, M, N)
+    plan.close()
+    assert_parity("WarpPerRowSmem", C_plan, a.rowptr, a.colidx, a.vals, B, None, 1.0, 0.0,
+                  rows=np.arange(0, M, 7), what="auto shape rule, plan")

@@ -29,7 +29,7 @@ __all__ = [
     "csrspmm_warp_per_row_fp4",
     "csrspmm_warp_per_row_smem_fp4",
 ]
-# Beyond the reference's five: the variant picked from N, an in-place product
+# Beyond the reference's five: the variant picked from the shape, an in-place product
 # with a real beta, a stored plan for repeated products with one A, and
 # device-side CSR tooling (torch.sparse_csr input, dense -> CSR, longest row).
 EXTRAS = ["csrspmm_auto", "csrspmm_spmm_out", "CsrSpmmPlan", "csrspmm_sparse", "from_sparse_csr",
@@ -58,7 +58,8 @@ def csrspmm_warp_per_row_smem_fp4(A_rowptr, A_colidx, A_values, A_max_row_nnz, B
 
 
 def csrspmm_auto(A_rowptr, A_colidx, A_values, B, alpha, beta):
-    """As the five entry points, with the variant picked from N."""
+    """As the five entry points, with the variant picked from the shape
+    (csrspmm_resolve_algorithm_ex)."""
     return _C.csrspmm_auto(A_rowptr, A_colidx, A_values, B, alpha, beta)
 
 
