@@ -306,7 +306,7 @@ def main():
 
     lib = capi.hip()
     resolved = lib.csrspmm_algorithm_name(
-        lib.csrspmm_resolve_algorithm_ex(capi.ALGO[args.algo], a.M, a.K, N, a.nnz)).decode()
+        lib.csrspmm_resolve_algorithm_ex(capi.ALGO[args.algo], a.M, a.K, N, a.nnz, -1)).decode()
     ms, main_ms = time_variant(capi, torch, args.algo, d, args.steps, args.warmup)
     print(f"[bench] {args.algo} ({resolved}): {ms:.4f} ms/call, main kernel {main_ms:.4f} ms",
           file=sys.stderr, flush=True)

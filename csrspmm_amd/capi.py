@@ -28,7 +28,7 @@ HIP_API = {
     "csrspmm_parse_algorithm": (_c_int, [ctypes.c_char_p]),
     "csrspmm_algorithm_name": (ctypes.c_char_p, [_c_int]),
     "csrspmm_resolve_algorithm": (_c_int, [_c_int, _c_int]),
-    "csrspmm_resolve_algorithm_ex": (_c_int, [_c_int] * 5),
+    "csrspmm_resolve_algorithm_ex": (_c_int, [_c_int] * 6),
     "csrspmm_workspace_bytes": (_c_size_t, [_c_int, _c_int, _c_int, _c_int]),
     "csrspmm_workspace_bytes_ex": (_c_size_t, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
     "csrspmm_workspace_panel_info": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int,

@@ -219,7 +219,17 @@ int owned_workspace_locked(void* stream, size_t bytes, void** out) {
 
 }  // namespace
 
-int resolve_algorithm(int algo, int M, int K, int N, int nnz) {
+int resolve_algorithm(int algo, int M, int K, int N, int nnz, int hint) {
+  if (algo == CSRSPMM_ALGO_AUTO && N % 4 == 0 && N < 128 && (long long)nnz >= 24LL * M &&
+      per_call_panels(4, wants_plan(CSRSPMM_ALGO_WARP_PER_ROW_FP4, M, nnz, hint), K, N, nnz, hint) > 0) {
+    // Below N = 128 the float4 form has the per-call column panels from a
+    // 64 MiB B, the scalar form none.  Measured on MI355X per call with the
+    // hint: power-law rows at K = 262144 (mean 32) N = 64 320.5 -> 227.4 us,
+    // N = 96 470.0 -> 295.9; mean 98 N = 64 896.9 -> 612.3.  R-MAT (15 per
+    // row, its panels turned off by the skew) stays scalar: 564 against 599 us
+    // at N = 64.
+    return CSRSPMM_ALGO_WARP_PER_ROW_FP4;
+  }
   if (algo == CSRSPMM_ALGO_AUTO && N % 4 == 0 && N == 128 && M >= 4096 &&
       (long long)K * N * 4 <= (4LL << 20) && (long long)nnz >= 160LL * M) {
     // A B that stays in the L2s and rows of 160 nonzeros or more on average:
@@ -351,7 +361,7 @@ int spmm_impl(int algo_in, int M, int K, int N, int nnz, const int* rowptr, cons
               const float* vals, int hint, const float* B, long long ldb, float* C, long long ldc,
               float alpha, float beta, unsigned flags, void* ws, size_t ws_bytes, bool owned,
               void* stream) {
-  const int algo = resolve_algorithm(algo_in, M, K, N, nnz);
+  const int algo = resolve_algorithm(algo_in, M, K, N, nnz, hint);
   Problem p;
   int st = fill_problem(p, algo, M, K, N, nnz, rowptr, colidx, vals, B, ldb, C, ldc, alpha, beta, flags);
   if (st != 0) return st;
@@ -521,8 +531,8 @@ const char* csrspmm_algorithm_name(int algo) {
 }
 
 int csrspmm_resolve_algorithm(int algo, int N) { return resolve_algorithm(algo, N); }
-int csrspmm_resolve_algorithm_ex(int algo, int M, int K, int N, int nnz) {
-  return resolve_algorithm(algo, M, K, N, nnz);
+int csrspmm_resolve_algorithm_ex(int algo, int M, int K, int N, int nnz, int max_row_nnz_hint) {
+  return resolve_algorithm(algo, M, K, N, nnz, max_row_nnz_hint);
 }
 
 size_t csrspmm_workspace_bytes(int algo, int M, int N, int nnz) {
@@ -534,7 +544,7 @@ size_t csrspmm_workspace_bytes(int algo, int M, int N, int nnz) {
 // The panels of a per-call product as far as the shape tells (pointer
 // alignment is checked per call); -1 when the call makes no plan.
 static int shape_panels(int algo, int M, int K, int N, int nnz, int hint) {
-  algo = resolve_algorithm(algo, M, K, N, nnz);
+  algo = resolve_algorithm(algo, M, K, N, nnz, hint);
   if (M <= 0 || N <= 0 || nnz < 0 || K < 0 || !wants_plan(algo, M, nnz, hint)) return -1;
   const bool fp4 = (algo == CSRSPMM_ALGO_WARP_PER_ROW_FP4 || algo == CSRSPMM_ALGO_WARP_PER_ROW_SMEM_FP4) &&
                    N % 4 == 0;

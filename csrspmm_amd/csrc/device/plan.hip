@@ -398,16 +398,20 @@ int csrspmm_plan_create(int algo, int M, int K, int nnz, const int* rowptr, cons
     return CSRSPMM_STATUS_INVALID_VALUE;
   if ((long long)M + nnz + 1 > 0x7fffffffLL - kMergeBlockMax) return CSRSPMM_STATUS_NOT_SUPPORTED;
   const int n_eff = n_hint > 0 ? n_hint : 128;
-  const int concrete = resolve_algorithm(algo, M, K, n_eff, nnz);
-  if (concrete < 0) return CSRSPMM_STATUS_INVALID_VALUE;
+  if (resolve_algorithm(algo, n_eff) < 0) return CSRSPMM_STATUS_INVALID_VALUE;
   hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));  // A must be ready
   if (e != hipSuccess) return (int)e;
   std::vector<int> rp((size_t)M + 1);
   e = hipMemcpy(rp.data(), rowptr, rp.size() * sizeof(int), hipMemcpyDeviceToHost);
   if (e != hipSuccess) return (int)e;
   if (rp[0] != 0 || rp[(size_t)M] != nnz) return CSRSPMM_STATUS_INVALID_CSR;
-  for (int r = 0; r < M; ++r)
+  int maxlen = 0;
+  for (int r = 0; r < M; ++r) {
     if (rp[(size_t)r + 1] < rp[(size_t)r]) return CSRSPMM_STATUS_INVALID_CSR;
+    maxlen = std::max(maxlen, rp[(size_t)r + 1] - rp[(size_t)r]);
+  }
+  // Auto from the shape and the true longest row
+  const int concrete = resolve_algorithm(algo, M, K, n_eff, nnz, maxlen);
   auto* p = new csrspmm_plan_s();
   p->algo = concrete;
   p->M = M;
@@ -419,8 +423,6 @@ int csrspmm_plan_create(int algo, int M, int K, int nnz, const int* rowptr, cons
   if (is_rowgroup_algorithm(concrete)) {
     const int vec = (concrete == CSRSPMM_ALGO_WARP_PER_ROW_FP4 ||
                      concrete == CSRSPMM_ALGO_WARP_PER_ROW_SMEM_FP4) && n_eff % 4 == 0 ? 4 : 1;
-    int maxlen = 0;
-    for (int r = 0; r < M; ++r) maxlen = std::max(maxlen, rp[(size_t)r + 1] - rp[(size_t)r]);
     p->maxlen = maxlen;
     p->use_plan = ((long long)M + nnz >= kPlanMinItems) || maxlen > kSegLen;
     p->dev_mode = p->use_plan && device_panels(p, vec, n_eff) > 0;

@@ -435,7 +435,7 @@ void bind_workspace(Problem& p, void* ws, const WorkspaceLayout& L, int mblk);
 
 // Shared by the per-call C ABI and stored plans (capi.hip).
 int resolve_algorithm(int algo, int N);  // CSRSPMM_ALGO_AUTO -> a concrete variant; -1 if invalid
-int resolve_algorithm(int algo, int M, int K, int N, int nnz);  // the same, from the whole shape
+int resolve_algorithm(int algo, int M, int K, int N, int nnz, int hint);  // the same, from the shape
 bool is_rowgroup_algorithm(int algo);
 bool uses_lds(int algo);
 int vector_width(int algo, const Problem& p);

@@ -110,7 +110,7 @@ def summarize(prof: str, name: str):
 
     lib = capi.hip()
     resolved = lib.csrspmm_algorithm_name(lib.csrspmm_resolve_algorithm_ex(
-        capi.ALGO[info["algo"]], info["M"], cfg.K(), info["N"], info["nnz"])).decode()
+        capi.ALGO[info["algo"]], info["M"], cfg.K(), info["N"], info["nnz"], -1)).decode()
     what = {"plan": "stored plan, ", "nopanels": "no column panels (base-size workspace), "}.get(
         info["mode"], "")
     lines = [

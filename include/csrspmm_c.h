@@ -81,12 +81,18 @@ const char* csrspmm_algorithm_name(int algo);
  * (a concrete id is returned unchanged; -1 for an invalid id). */
 int csrspmm_resolve_algorithm(int algo, int N);
 /* The concrete variant CSRSPMM_ALGO_AUTO runs for the whole shape (A is
- * M x K with nnz nonzeros, N output columns): csrspmm_resolve_algorithm's
- * choice, except that at N = 128 a B of at most 4 MiB with rows of 160 or
- * more nonzeros on average (M >= 4096) takes the scalar LDS-staged variant.
- * The SpMM entry points and stored plans resolve Auto this way.  No
- * counterpart in the reference, whose Auto stub is empty. */
-int csrspmm_resolve_algorithm_ex(int algo, int M, int K, int N, int nnz);
+ * M x K with nnz nonzeros, N output columns, max_row_nnz_hint as for the
+ * SpMM, -1 if unknown): csrspmm_resolve_algorithm's choice, except that
+ *  - below N = 128 (N % 4 == 0), rows of 24 or more nonzeros on average
+ *    with per-call column panels possible for float4 columns (a B of at
+ *    least 64 MiB, a row of 1024 or more not ruled out) take the float4
+ *    broadcast variant, which has the panels;
+ *  - at N = 128 a B of at most 4 MiB with rows of 160 or more nonzeros on
+ *    average (M >= 4096) takes the scalar LDS-staged variant.
+ * The SpMM entry points resolve Auto this way, and stored plans with the
+ * true longest row.  No counterpart in the reference, whose Auto stub is
+ * empty. */
+int csrspmm_resolve_algorithm_ex(int algo, int M, int K, int N, int nnz, int max_row_nnz_hint);
 
 /* Bytes of device workspace csrspmm_spmm_f32_ws needs for this problem
  * (row-split plan, partial sums of split rows, counters).  No counterpart in

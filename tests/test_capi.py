@@ -52,15 +52,26 @@ def test_parse_and_names():
     assert lib.csrspmm_resolve_algorithm(9, 128) == -1
     # From the whole shape: at N = 128 an L2-sized B (<= 4 MiB) with long rows
     # (>= 160 per row on average, M >= 4096) takes WarpPerRowSmem
-    ex = lib.csrspmm_resolve_algorithm_ex
+    def ex(a, M, K, N, nnz, hint=-1):
+        return lib.csrspmm_resolve_algorithm_ex(a, M, K, N, nnz, hint)
     assert ex(6, 4096, 4096, 128, 4096 * 160) == 4
     assert ex(6, 4096, 8192, 128, 4096 * 160) == 4          # B exactly 4 MiB
     assert ex(6, 4096, 8193, 128, 4096 * 160) == 3          # B above 4 MiB
     assert ex(6, 4096, 4096, 128, 4096 * 160 - 1) == 3      # rows shorter
     assert ex(6, 4095, 4096, 128, 4095 * 200) == 3          # fewer rows
     assert ex(6, 4096, 4096, 256, 4096 * 200) == 3          # N = 256
-    assert ex(6, 4096, 4096, 64, 4096 * 200) == 4           # below 128: scalar anyway
     assert ex(6, 262144, 262144, 128, 8453223) == 3         # XL
+    # below N = 128: float4 when its column panels are possible (B >= 64 MiB,
+    # no hint below 1024) and rows average 24 or more
+    assert ex(6, 262144, 262144, 64, 8453223) == 3          # XL at N = 64: 64 MiB
+    assert ex(6, 262144, 262144, 96, 8453223) == 3
+    assert ex(6, 262144, 262144, 60, 8453223) == 4          # 60 MiB: no panels
+    assert ex(6, 262144, 262144, 64, 8453223, 1023) == 4    # hint rules panels out
+    assert ex(6, 262144, 262144, 64, 8453223, 16315) == 3
+    assert ex(6, 262144, 262144, 64, 24 * 262144 - 1) == 4  # rows shorter
+    assert ex(6, 1 << 20, 1 << 20, 64, 16 << 20) == 4       # R-MAT-like: 16 per row
+    assert ex(6, 262144, 262144, 66, 8453223) == 4          # N % 4 != 0
+    assert ex(6, 4096, 4096, 64, 4096 * 200) == 4           # small B: scalar
     assert ex(3, 4096, 4096, 128, 4096 * 200) == 3          # concrete ids pass through
     assert ex(9, 4096, 4096, 128, 4096 * 200) == -1
     assert lib.csrspmm_version() >= 100
@@ -206,7 +217,8 @@ def test_panel_rules_without_device():
     assert panels("WarpPerRowSmemFp4", M, 65536, 128, nnz) == 0      # 32 MiB
     assert panels("WarpPerRowSmem", M, 262144, 128, nnz) == 64       # scalar columns from N = 128
     assert panels("WarpPerRowSmem", M, 262144, 64, nnz) == 0         # but not at N = 64
-    assert panels("Auto", M, 262144, 64, nnz) == 0                   # Auto runs the scalar form there
+    assert panels("Auto", M, 262144, 64, nnz) == 32                  # Auto takes float4 for them
+    assert panels("Auto", M, 262144, 64, nnz, 1023) == 0             # unless no row can use them
     assert panels("Auto", M, 262144, 128, nnz) == 64
     assert panels("WarpPerRowSmemFp4", M, 65536, 256, nnz) == 0      # 16 MiB bands: column slices
     assert panels("WarpPerRowSmemFp4", M, 131072, 256, nnz) == 64    # 32 MiB bands: panels

@@ -25,12 +25,17 @@ TOL = 1e-5
 PANEL_ALGOS = ["WarpPerRowFp4", "WarpPerRowSmemFp4", "Auto", "WarpPerRow", "WarpPerRowSmem"]
 
 
-def expects_panels(algo, N):
+def expects_panels(algo, N, M=None, K=None, nnz=None):
     """Whether a per-call product on a 64 MiB+ B with N <= 256 takes panels:
-    float4 columns at any N, scalar columns (Auto below N = 128 included) from
-    N = 128."""
+    float4 columns at any N, scalar columns from N = 128.  Auto is resolved
+    from the shape by the library (below N = 128 it takes float4 columns
+    when rows average 24 nonzeros or more)."""
+    if algo == "Auto":
+        lib = capi.hip()
+        algo = lib.csrspmm_algorithm_name(
+            lib.csrspmm_resolve_algorithm_ex(capi.ALGO["Auto"], M, K, N, nnz, -1)).decode()
     return algo in ("WarpPerRowFp4", "WarpPerRowSmemFp4") or (
-        algo in ("WarpPerRow", "WarpPerRowSmem", "Auto") and N >= 128)
+        algo in ("WarpPerRow", "WarpPerRowSmem") and N >= 128)
 
 
 def run(algo, rowptr, colidx, vals, B, dev, C0=None, alpha=1.0, beta=0.0, workspace_bytes=None):
@@ -85,7 +90,7 @@ def test_panels_mixed_rows(algo, N, gpu):
     B = gen.dense(11, gen.TAG_B, K, N)
     print(f"[panels] mixed {algo} N={N} M={lens.size} nnz={colidx.size}", flush=True)
     base, full = panel_bytes(algo, lens.size, K, N, colidx.size)
-    if expects_panels(algo, N):
+    if expects_panels(algo, N, lens.size, K, colidx.size):
         assert full > base, "a 64 MiB B reserves the panel tables"
     else:
         assert full == base
@@ -195,7 +200,7 @@ def test_panels_odd_k(algo, K, gpu):
     rowptr, colidx, vals = csr_from_lengths(lens, K, seed=K)
     B = gen.dense(16, gen.TAG_B, K, N)
     base, full = panel_bytes(algo, lens.size, K, N, colidx.size)
-    if expects_panels(algo, N):
+    if expects_panels(algo, N, lens.size, K, colidx.size):
         assert full > base
     C = run(algo, rowptr, colidx, vals, B, gpu)
     check(algo, C, rowptr, colidx, vals, B, what=f"K={K}")

@@ -118,7 +118,7 @@ def test_auto_takes_scalar_lds_on_l2_sized_long_rows(gpu):
     M, K, N = 4096, 4096, 128
     a = gen.uniform(M, K, 200, 21)
     B = gen.dense(21, gen.TAG_B, K, N)
-    ex = capi.hip().csrspmm_resolve_algorithm_ex(capi.ALGO["Auto"], M, K, N, a.nnz)
+    ex = capi.hip().csrspmm_resolve_algorithm_ex(capi.ALGO["Auto"], M, K, N, a.nnz, -1)
     assert capi.hip().csrspmm_algorithm_name(ex).decode() == "WarpPerRowSmem"
     from test_gpu_parity import run_spmm
     C_auto = run_spmm("Auto", a.rowptr, a.colidx, a.vals, B, gpu)
