@@ -281,6 +281,7 @@ int fill_problem(Problem& p, int algo, int M, int K, int N, int nnz, const int* 
   if (algo < 0 || algo >= CSRSPMM_ALGO_COUNT) return CSRSPMM_STATUS_INVALID_VALUE;
   if (M < 0 || K < 0 || N < 0 || nnz < 0) return CSRSPMM_STATUS_INVALID_VALUE;
   p = Problem{};
+  p.row_hint = -1;
   p.M = M;
   p.K = K;
   p.N = N;

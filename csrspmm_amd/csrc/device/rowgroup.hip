@@ -359,12 +359,12 @@ __device__ __forceinline__ void stream_rows(const Problem& p, const Panel<VEC, G
 // columns.  A row with a column out of order or out of range takes all its
 // nonzeros in band 0, in CSR order.  A row longer than long_row is skipped
 // (its segments are summed elsewhere) unless the rows are summed whole.
-template <int R>
-__device__ __forceinline__ void sweep_rows(const Problem& p, const Panel<4, 16, 1, true>& pn, int unit,
+template <int G, int R>
+__device__ __forceinline__ void sweep_rows(const Problem& p, const Panel<4, G, 1, true>& pn, int unit,
                                            int gl, int gbase, int* bnd) {
-  constexpr int G = 16;
+  static_assert(G == 16 || G == 32, "sweep groups of 16 or 32 lanes");
   constexpr int NB1 = kSweepMaxBands + 1;
-  const unsigned long long gmask = 0xFFFFull << gbase;
+  const unsigned long long gmask = ((1ull << G) - 1ull) << gbase;
   const int nb = p.sweep_bands;
   const int sh = p.sweep_shift;
   bool keep[R];
@@ -612,10 +612,12 @@ __device__ __forceinline__ void rowgroup_block(const Problem& p, int bid, int se
 
   const int unit = (bid - seg_blocks) * GPB + gid;
   if constexpr (SWEEP) {
-    // The band sweep of a column slice: kSweepRows rows per group.
-    static_assert(VEC == 4 && G == 16 && T == 1 && BUF, "the sweep runs 64-column float4 slices");
+    // The band sweep of a column slice (or of all N <= 128 columns):
+    // kSweepRows rows per group.
+    static_assert(VEC == 4 && (G == 16 || G == 32) && T == 1 && BUF,
+                  "the sweep runs float4 groups of up to 128 columns");
     const Panel<VEC, G, T, BUF> pn(p, c_lo, gl, c_hi);
-    sweep_rows<kSweepRows>(p, pn, unit, gl, gbase, sweep_bnd + gid * kSweepRows * (kSweepMaxBands + 1));
+    sweep_rows<G, kSweepRows>(p, pn, unit, gl, gbase, sweep_bnd + gid * kSweepRows * (kSweepMaxBands + 1));
     return;
   }
   if (p.plan) {
@@ -1070,11 +1072,36 @@ static inline int pow2_ceil(int x) {
 }
 
 // Unsliced float4 calls: the group width from N.
+// Unsliced float4 calls of up to 128 columns sweep too when B exceeds
+// CSRSPMM_SWEEP_UNSLICED_MB and the max_row_nnz hint rules out skewed rows
+// (longest row at most long_row or 4x the mean).  Measured on MI355X per
+// call, bit-identical: uniform rows with the hint, 32768^2 x 128 with 40 per
+// row 77.1 -> 48.8 us, 65536^2 x 64 with 32 per row 67.0 -> 49.1 us,
+// 16384^2 x 128 with 20 per row 24.0 -> 21.7 us, medium (82 per row, 8 MiB)
+// 49.5 -> 50.8 us; power-law rows (mean 32, the hint excludes them) lost
+// 8-19% swept.
+#ifndef CSRSPMM_SWEEP_UNSLICED_MB
+#define CSRSPMM_SWEEP_UNSLICED_MB 4
+#endif
 template <bool LDS, bool BUF>
 static hipError_t dispatch_vec4_cols(const Problem& p, hipStream_t s) {
   constexpr int SU = CSRSPMM_SEG_UNROLL;
   const int nv = p.N / 4;
   const int G = nv >= 64 ? 64 : (pow2_ceil(nv) < 4 ? 4 : pow2_ceil(nv));
+  if constexpr (!LDS && BUF) {
+    const long long mean4 = p.M > 0 ? 4LL * p.nnz / p.M : 0;
+    if ((G == 16 || G == 32) && p.dp.P == 0 && p.row_hint >= 0 &&
+        p.row_hint <= std::max<long long>(p.long_row, mean4) &&
+        (long long)p.K * p.N * 4 > ((long long)CSRSPMM_SWEEP_UNSLICED_MB << 20) &&
+        sweep_applies(p.plan, p.M, p.K, p.nnz, G * 4)) {
+      Problem q = p;
+      sweep_geometry(p.K, G * 4, q.sweep_shift, q.sweep_bands);
+      if (q.sweep_bands >= 2) {
+        if (G == 16) return launch_rg<4, 16, 1, kVec4U, false, CSRSPMM_SWEEP_SU, true, true>(q, s);
+        return launch_rg<4, 32, 1, kVec4U, false, CSRSPMM_SWEEP_SU, true, true>(q, s);
+      }
+    }
+  }
   if (G < 64) {
     switch (G) {
       case 4: return launch_rg<4, 4, 1, kVec4U, LDS, SU, BUF>(p, s);

@@ -355,6 +355,9 @@ struct Problem {
   // Band sweep of the short rows of a column slice (sweep_geometry; bands 0:
   // merge blocks instead): bands of 2^sweep_shift B rows, sweep_bands of them.
   int sweep_shift, sweep_bands;
+  // The caller's max_row_nnz hint (or a stored plan's true longest row);
+  // -1 when unknown.
+  int row_hint;
 };
 
 // Band sweep (sliced float4 calls).  Each group keeps kSweepRows rows'
@@ -386,9 +389,20 @@ inline void sweep_geometry(int K, int sw, int& shift, int& bands) {
 #ifndef CSRSPMM_SWEEP_MIN_PER_BAND
 #define CSRSPMM_SWEEP_MIN_PER_BAND 2
 #endif
+// A group keeps one gather per row in flight, so the sweep also needs
+// enough groups to hide latency: at least 8192 waves for 16-lane groups (64
+// columns) and 4096 for 32-lane ones.  Measured on MI355X per call against
+// the merge blocks, K = 65536 x 256 sliced with 66 per row: M = 8192 (1024
+// waves) 74 -> 170 us, 16384 101 -> 176, 32768 (4096 waves) 183 -> 190,
+// 65536 (8192 waves) 380 -> 305; unsliced K = 32768 x 128 with 100 per row:
+// M = 8192 (2048 waves) 38 -> 55, 12288 55 -> 56, 16384 (4096 waves) 75 ->
+// 59, 24576 115 -> 69.
 inline bool sweep_applies(bool plan, int M, int K, int nnz, int sw,
                           int min_per_band = CSRSPMM_SWEEP_MIN_PER_BAND) {
   if (!plan || sw <= 0 || M <= 0 || K <= 0) return false;
+  const int G = sw / 4;  // lanes per group, float4 columns
+  const long long waves = (long long)M / kSweepRows * G / 64;
+  if (waves < (G >= 32 ? 4096 : 8192)) return false;
   int shift, bands;
   sweep_geometry(K, sw, shift, bands);
   return (long long)nnz >= (long long)min_per_band * bands * M;
@@ -408,6 +422,7 @@ __host__ __device__ inline int seg_count(const Problem& p, int len) {
 
 // The hint flags for a longest row of max_row_nnz nonzeros (-1: unknown).
 inline void set_row_hint(Problem& p, int max_row_nnz) {
+  p.row_hint = max_row_nnz < 0 ? -1 : max_row_nnz;
   p.rows_whole = max_row_nnz >= 0 && max_row_nnz <= p.long_row;
   p.no_split = max_row_nnz >= 0 && max_row_nnz < (2 << p.seg_shift);
   if (p.rows_whole) p.nslots = 0;

@@ -1,9 +1,10 @@
 """The band sweep of column slices (rowgroup.hip sweep_rows): float4 calls of
 the register variant whose B is sliced (B of at least 32 MiB, N >= 128, a
-64-column band of at most 16 MiB) and whose rows average at least two
-nonzeros per band keep two rows' accumulators per 16-lane group while all
-groups walk B in bands.  Every shape below meets those conditions
-(K = 32768 or 49152, bands of 16384 B rows).  Each case is checked against
+64-column band of at most 16 MiB), whose rows average at least two
+nonzeros per band and which have enough rows for 8192 waves (M >= 65536)
+keep two rows' accumulators per 16-lane group while all groups walk B in
+bands.  Every shape below meets those conditions (K = 32768 or 49152, bands
+of 16384 B rows).  Each case is checked against
 the oracle on every row, and against the LDS-staged variant
 (WarpPerRowSmemFp4), which keeps the merge blocks: both sum every short row
 whole in CSR order and the long rows in the same segments, so the two must
@@ -68,12 +69,14 @@ def run(algo, gpu, rp, ci, va, B, C0, alpha, beta, hint=-1):
     return dC
 
 
+MS = 65536  # rows: 8192 waves of two rows per 16-lane group
+
 CASES = {
     # id: (M, K, N, long rows (row, length), unsorted rows)
-    "ragged": (3000, 32768, 256, (), ()),
-    "long_rows": (3000, 32768, 256, ((7, 300), (1500, 2500), (2999, 129)), ()),
-    "unsorted": (3000, 32768, 256, ((11, 700),), (3, 4, 11, 2000)),
-    "narrow_last_slice": (2000, 49152, 200, ((5, 400),), (9,)),
+    "ragged": (MS, 32768, 256, (), ()),
+    "long_rows": (MS, 32768, 256, ((7, 300), (1500, 2500), (MS - 1, 129)), ()),
+    "unsorted": (MS, 32768, 256, ((11, 700),), (3, 4, 11, 2000)),
+    "narrow_last_slice": (MS, 49152, 200, ((5, 400),), (9,)),
 }
 
 
@@ -98,7 +101,7 @@ def test_sweep_with_hints(hint, gpu):
     """max_row_nnz = the true longest row (>= 128: segments as without a
     hint), and a hint of 90 with rows up to 300 long: every row is then summed
     whole, the long ones by the sweep itself."""
-    M, K, N = 3000, 32768, 256
+    M, K, N = MS, 32768, 256
     rp, ci, va = rows_csr(lengths_for(M, 9, ((17, 300), (2400, 250))), K, 10)
     rng = np.random.default_rng(11)
     B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
@@ -112,7 +115,7 @@ def test_sweep_with_hints(hint, gpu):
 
 def test_sweep_strided_operands(gpu):
     """B and C as column windows of wider tensors (ldb, ldc > N)."""
-    M, K, N = 2500, 32768, 256
+    M, K, N = MS, 32768, 256
     rp, ci, va = rows_csr(lengths_for(M, 12, ((40, 333),)), K, 13)
     rng = np.random.default_rng(14)
     Bw = rng.uniform(-1, 1, (K, N + 12)).astype(np.float32)
@@ -130,7 +133,7 @@ def test_sweep_stored_plan(gpu):
     """A stored plan of a matrix whose long rows stay below the panel
     threshold (1024): the plan's calls slice and sweep like the per-call path
     and must match it bit for bit."""
-    M, K, N = 3000, 32768, 256
+    M, K, N = MS, 32768, 256
     rp, ci, va = rows_csr(lengths_for(M, 15, ((100, 900), (101, 140))), K, 16, (50,))
     rng = np.random.default_rng(17)
     B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
@@ -154,8 +157,8 @@ def test_sweep_wide_band_with_hint(gpu):
     panels can apply, as with a max_row_nnz hint below 1024.  Checked against
     the oracle and, bit for bit, against the LDS-staged variant, which stays
     unsliced there."""
-    M, K, N = 2000, 81920, 256
-    rp, ci, va = rows_csr(lengths_for(M, 18, ((3, 300), (1999, 700))), K, 19, (8,))
+    M, K, N = MS, 81920, 256
+    rp, ci, va = rows_csr(lengths_for(M, 18, ((3, 300), (MS - 1, 700))), K, 19, (8,))
     rng = np.random.default_rng(20)
     B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
     C0 = rng.uniform(-1, 1, (M, N)).astype(np.float32)
@@ -164,3 +167,29 @@ def test_sweep_wide_band_with_hint(gpu):
     check_all(C.cpu().numpy(), rp, ci, va, B, -1.25, 0.5, C0, "wide band")
     ref = run("WarpPerRowSmemFp4", gpu, rp, ci, va, B, C0, -1.25, 0.5, hint=h)
     assert torch.equal(C, ref)
+
+
+@pytest.mark.parametrize("N", [128, 64])
+def test_unsliced_sweep_with_hint(N, gpu):
+    """Float4 calls of up to 128 columns also sweep when B exceeds 4 MiB, the
+    max_row_nnz hint rules out skewed rows (at most 128, or 4x the mean) and
+    the rows fill enough waves (M = 16384 with 32-lane groups, 65536 with
+    16-lane ones):
+    K = 32768 gives a 16 MiB (N = 128) or 8 MiB (N = 64) B in 4 MiB bands.
+    Rows of 50-149 nonzeros with one of 300 (segments, skipped by the sweep;
+    the hint 300 is below 4x the mean) and one unsorted.  Against the oracle
+    and bit for bit against the merge blocks."""
+    M, K = (16384 if N == 128 else MS), 32768  # 4096 / 8192 waves
+    rng = np.random.default_rng(22)
+    lens = rng.integers(50, 150, M)
+    lens[17] = 300
+    rp, ci, va = rows_csr(lens, K, 23, (40,))
+    B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+    C0 = rng.uniform(-1, 1, (M, N)).astype(np.float32)
+    h = int(np.diff(rp).max())
+    C = run("WarpPerRowFp4", gpu, rp, ci, va, B, C0, 0.5, -2.0, hint=h)
+    check_all(C.cpu().numpy(), rp, ci, va, B, 0.5, -2.0, C0, f"unsliced N={N}")
+    ref = run("WarpPerRowSmemFp4", gpu, rp, ci, va, B, C0, 0.5, -2.0, hint=h)
+    assert torch.equal(C, ref)
+    no_hint = run("WarpPerRowFp4", gpu, rp, ci, va, B, C0, 0.5, -2.0)
+    assert torch.equal(C, no_hint)
