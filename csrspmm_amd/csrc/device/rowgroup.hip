@@ -345,9 +345,10 @@ __device__ __forceinline__ void stream_rows(const Problem& p, const Panel<VEC, G
   }
 }
 
-// Band sweep of the short rows of one column slice (float4, 16-lane groups,
-// B through a buffer resource).  The group owns rows [unit R, unit R + R)
-// and keeps their accumulators in registers through the whole slice.  All
+// Band sweep of the short rows of one column slice, or of all N <= 128
+// columns (float4, 16- or 32-lane groups, B through a buffer resource).  The
+// group owns rows [unit R, unit R + R) and keeps their accumulators in
+// registers through the whole slice.  All
 // groups start together and walk B in bands of 2^sweep_shift rows: in band
 // b each row takes its nonzeros whose columns fall in the band, so at any
 // time the running groups gather from about one band, which stays in the
