@@ -193,3 +193,26 @@ def test_unsliced_sweep_with_hint(N, gpu):
     assert torch.equal(C, ref)
     no_hint = run("WarpPerRowFp4", gpu, rp, ci, va, B, C0, 0.5, -2.0)
     assert torch.equal(C, no_hint)
+
+
+@pytest.mark.parametrize("seed,M,K,N", [(31, 70000, 48000, 192), (32, 66000, 30000, 320),
+                                        (33, 80000, 65000, 132)])
+def test_sweep_random_shapes(seed, M, K, N, gpu):
+    """Seeded shapes off the powers of two (rows and slices that do not
+    divide evenly, a last slice of 4 columns at N = 132), with a few long
+    and unsorted rows: bit for bit against the merge blocks, and against the
+    oracle on sampled rows."""
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(0, 2 * (seed % 5 + 20), M)
+    for r in rng.choice(M, 6, replace=False):
+        lens[r] = int(rng.integers(129, 3000))
+    rp, ci, va = rows_csr(lens, K, seed + 100, tuple(int(x) for x in rng.choice(M, 4, replace=False)))
+    B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+    C0 = rng.uniform(-1, 1, (M, N)).astype(np.float32)
+    C = run("WarpPerRowFp4", gpu, rp, ci, va, B, C0, 1.0, 1.0)
+    ref = run("WarpPerRowSmemFp4", gpu, rp, ci, va, B, C0, 1.0, 1.0)
+    assert torch.equal(C, ref)
+    rows = np.unique(np.concatenate([rng.choice(M, 3000, replace=False), np.nonzero(lens > 128)[0]]))
+    R, S = oracle.spmm_f64(rp, ci, va, B, C0, 1.0, 1.0, rows=rows)
+    bad, ratio, _, _ = oracle.check(C.cpu().numpy()[rows], R, S, 1e-5)
+    assert bad == 0, f"{bad} elements off, max ratio {ratio}"
