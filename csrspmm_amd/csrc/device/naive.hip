@@ -22,6 +22,15 @@ namespace {
 
 constexpr int kNaiveWaves = 4;
 constexpr int kNaiveUnroll = 8;
+// A long row is one wave's (or block's) chain of dependent batches: batches
+// of kNaiveLongUnroll gathers in flight come before the 8-wide ones and the
+// tail.  Measured on MI355X per call against 8 throughout: Naive XL 1878 ->
+// 1380 us, R-MAT N = 64 4593 -> 3130 us, medium 63.7 -> 57.8 us; NaiveSmem
+// XL 1792 -> 1451 us, R-MAT 3858 -> 2913 us (16 or 64 in flight: slower).
+#ifndef CSRSPMM_NAIVE_LONG_UNROLL
+#define CSRSPMM_NAIVE_LONG_UNROLL 32
+#endif
+constexpr int kNaiveLongUnroll = CSRSPMM_NAIVE_LONG_UNROLL;
 
 __global__ __launch_bounds__(kNaiveWaves * 64) void naive_kernel(Problem p, int ntile) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -36,20 +45,25 @@ __global__ __launch_bounds__(kNaiveWaves * 64) void naive_kernel(Problem p, int 
   const float* bc = p.B + col;
   float sum = 0.0f;
   int j = start;
-  for (; j + kNaiveUnroll <= end; j += kNaiveUnroll) {
-    int c[kNaiveUnroll];
-    float v[kNaiveUnroll];
-    float b[kNaiveUnroll];
+  // U gathers of the row in flight, then the next U, in CSR order
+  auto batch = [&](auto u_const) {
+    constexpr int U = decltype(u_const)::value;
+    int c[U];
+    float v[U];
+    float b[U];
 #pragma unroll
-    for (int u = 0; u < kNaiveUnroll; ++u) {
+    for (int u = 0; u < U; ++u) {
       c[u] = p.colidx[j + u];
       v[u] = p.vals[j + u];
     }
 #pragma unroll
-    for (int u = 0; u < kNaiveUnroll; ++u) b[u] = valid ? bc[(long long)c[u] * p.ldb] : 0.0f;
+    for (int u = 0; u < U; ++u) b[u] = valid ? bc[(long long)c[u] * p.ldb] : 0.0f;
 #pragma unroll
-    for (int u = 0; u < kNaiveUnroll; ++u) sum = __builtin_fmaf(v[u], b[u], sum);
-  }
+    for (int u = 0; u < U; ++u) sum = __builtin_fmaf(v[u], b[u], sum);
+    j += U;
+  };
+  while (j + kNaiveLongUnroll <= end) batch(std::integral_constant<int, kNaiveLongUnroll>{});
+  while (j + kNaiveUnroll <= end) batch(std::integral_constant<int, kNaiveUnroll>{});
   for (; j < end; ++j) {
     const int c = p.colidx[j];
     const float v = p.vals[j];
@@ -85,14 +99,17 @@ __global__ __launch_bounds__(256) void naive_smem_kernel(Problem p, int ntile, i
     }
     __syncthreads();
     int k = 0;
-    for (; k + kNaiveUnroll <= cnt; k += kNaiveUnroll) {
-      float b[kNaiveUnroll];
+    auto batch = [&](auto u_const) {
+      constexpr int U = decltype(u_const)::value;
+      float b[U];
 #pragma unroll
-      for (int u = 0; u < kNaiveUnroll; ++u)
-        b[u] = valid ? bc[(long long)s_col[k + u] * p.ldb] : 0.0f;
+      for (int u = 0; u < U; ++u) b[u] = valid ? bc[(long long)s_col[k + u] * p.ldb] : 0.0f;
 #pragma unroll
-      for (int u = 0; u < kNaiveUnroll; ++u) sum = __builtin_fmaf(s_val[k + u], b[u], sum);
-    }
+      for (int u = 0; u < U; ++u) sum = __builtin_fmaf(s_val[k + u], b[u], sum);
+      k += U;
+    };
+    while (k + kNaiveLongUnroll <= cnt) batch(std::integral_constant<int, kNaiveLongUnroll>{});
+    while (k + kNaiveUnroll <= cnt) batch(std::integral_constant<int, kNaiveUnroll>{});
     for (; k < cnt; ++k) {
       const float b = valid ? bc[(long long)s_col[k] * p.ldb] : 0.0f;
       sum = __builtin_fmaf(s_val[k], b, sum);
