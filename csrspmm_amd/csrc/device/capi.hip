@@ -374,7 +374,7 @@ int spmm_impl(int algo_in, int M, int K, int N, int nnz, const int* rowptr, cons
   if (p.plan) {
     const int vec = vector_width(algo, p);
     int P = per_call_panels(vec, true, K, N, nnz, hint);
-    p.sw = slice_width(K, N, P > 0, wide_sweep(vec, uses_lds(algo), true, M, K, nnz));
+    p.sw = slice_width(K, N, P > 0, wide_sweep(vec, true, M, K, nnz));
     p.slice_launch = slice_launches(M, nnz);
     if (p.sw > 0) P = 0;  // a sliced call gathers band by band instead
     WorkspaceLayout L = workspace_layout(M, K, N, nnz, P);

@@ -481,7 +481,7 @@ int csrspmm_plan_spmm_f32(csrspmm_plan_t plan, int N, const float* B, long long 
     pr.dp_ready = true;
     pr.sw = P > 0 ? 0
                   : slice_width(p->K, N, false,
-                                wide_sweep(vec, uses_lds(p->algo), true, p->M, p->K, p->nnz));
+                                wide_sweep(vec, true, p->M, p->K, p->nnz));
     pr.slice_launch = slice_launches(p->M, p->nnz);
     return to_status(launch_algorithm(p->algo, pr, s));
   }
@@ -502,7 +502,7 @@ int csrspmm_plan_spmm_f32(csrspmm_plan_t plan, int N, const float* B, long long 
   const bool lds = uses_lds(p->algo);
   // a plan with panelized rows keeps them; otherwise large B are sliced by columns
   pr.sw = p->npan > 0 ? 0
-                      : slice_width(p->K, N, false, wide_sweep(vec, lds, true, p->M, p->K, p->nnz));
+                      : slice_width(p->K, N, false, wide_sweep(vec, true, p->M, p->K, p->nnz));
   pr.slice_launch = slice_launches(p->M, p->nnz);
   pr.pan_rows = p->d_pan_rows;
   pr.pan_ptr = p->d_pan_ptr;

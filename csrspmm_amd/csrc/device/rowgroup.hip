@@ -29,9 +29,9 @@
 //    flight across row boundaries and a row's accumulator is flushed
 //    (epilogue + store) when the stream passes its end.  With column slices
 //    the segment and merge blocks repeat per slice of columns; float4
-//    slices of the register variant replace the merge blocks by a band
-//    sweep (sweep_rows), whose groups keep their rows for the whole slice
-//    and gather from B band after band.
+//    slices replace the merge blocks by a band sweep (sweep_rows), whose
+//    groups keep their rows for the whole slice and gather from B band
+//    after band.
 //  * combine_kernel: adds each split or panelized row's partials in a
 //    fixed order.
 // Everything is deterministic (no float atomics): results repeat bit for bit.
@@ -360,9 +360,9 @@ __device__ __forceinline__ void stream_rows(const Problem& p, const Panel<VEC, G
 // columns.  A row with a column out of order or out of range takes all its
 // nonzeros in band 0, in CSR order.  A row longer than long_row is skipped
 // (its segments are summed elsewhere) unless the rows are summed whole.
-template <int G, int R>
+template <int G, int R, bool LDS>
 __device__ __forceinline__ void sweep_rows(const Problem& p, const Panel<4, G, 1, true>& pn, int unit,
-                                           int gl, int gbase, int* bnd) {
+                                           int gl, int gbase, int* bnd, int2* stage) {
   static_assert(G == 16 || G == 32, "sweep groups of 16 or 32 lanes");
   constexpr int NB1 = kSweepMaxBands + 1;
   const unsigned long long gmask = ((1ull << G) - 1ull) << gbase;
@@ -436,6 +436,12 @@ __device__ __forceinline__ void sweep_rows(const Problem& p, const Panel<4, G, 1
       int cj[R];
       float vj[R];
       load_chunk_rows(b, base, cj, vj);
+      if constexpr (LDS) {
+        // the LDS-staged variant: each row's chunk through the wave's stage
+#pragma unroll
+        for (int r = 0; r < R; ++r) stage[r * 64 + gbase + gl] = make_int2(cj[r], __float_as_int(vj[r]));
+        wave_lds_sync();
+      }
       // One gather per row in flight at a time: measured on MI355X (65536 x
       // 65536 x 256, 66 per row), 2 rows x 1 ran 286 us, 2 x 2 427 us, 1 x 2
       // 310 us, 1 x 4 477 us.  An entry past a row's count gets an offset
@@ -450,8 +456,15 @@ __device__ __forceinline__ void sweep_rows(const Problem& p, const Panel<4, G, 1
         float v[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-          const int c = group_bcast<G>(cj[r], gbase, k);
-          v[r] = group_bcast<G>(vj[r], gbase, k);
+          int c;
+          if constexpr (LDS) {
+            const int2 e = stage[r * 64 + gbase + k];
+            c = e.x;
+            v[r] = __int_as_float(e.y);
+          } else {
+            c = group_bcast<G>(cj[r], gbase, k);
+            v[r] = group_bcast<G>(vj[r], gbase, k);
+          }
           const unsigned off =
               base + k < cnt[r] ? __umul24((unsigned)c, pn.bb.rowbytes) + pn.colbytes[0] : kBufOffPast;
           bv[r] = ld_b_buf<4>(pn.bb, off);
@@ -459,6 +472,7 @@ __device__ __forceinline__ void sweep_rows(const Problem& p, const Panel<4, G, 1
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[r] = fma_v(v[r], bv[r], acc[r]);
       }
+      if constexpr (LDS) wave_lds_sync();  // the chunk is read before the next overwrites it
     }
   }
 #pragma unroll
@@ -618,7 +632,8 @@ __device__ __forceinline__ void rowgroup_block(const Problem& p, int bid, int se
     static_assert(VEC == 4 && (G == 16 || G == 32) && T == 1 && BUF,
                   "the sweep runs float4 groups of up to 128 columns");
     const Panel<VEC, G, T, BUF> pn(p, c_lo, gl, c_hi);
-    sweep_rows<G, kSweepRows>(p, pn, unit, gl, gbase, sweep_bnd + gid * kSweepRows * (kSweepMaxBands + 1));
+    sweep_rows<G, kSweepRows, LDS>(p, pn, unit, gl, gbase, sweep_bnd + gid * kSweepRows * (kSweepMaxBands + 1),
+                                   stage);
     return;
   }
   if (p.plan) {
@@ -714,8 +729,11 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(SWE
   const int gbase = lane & ~(G - 1);
   const int gid = wave * GPW + lane / G;  // group index within block
 
-  __shared__ int2 stage_all[LDS ? kWaves * 64 : 1];
-  int2* stage = stage_all + (LDS ? wave * 64 : 0);
+  // the LDS variants' per-wave stage: 64 (col, val) pairs, one row's chunk
+  // each for the sweep's kSweepRows rows
+  constexpr int kStage = 64 * (SWEEP ? kSweepRows : 1);
+  __shared__ int2 stage_all[LDS ? kWaves * kStage : 1];
+  int2* stage = stage_all + (LDS ? wave * kStage : 0);
   // band starts of the sweep's rows, kSweepRows x (kSweepMaxBands + 1) per group
   __shared__ int sweep_bnd[SWEEP ? kWaves * GPW * kSweepRows * (kSweepMaxBands + 1) : 1];
 
@@ -1089,7 +1107,7 @@ static hipError_t dispatch_vec4_cols(const Problem& p, hipStream_t s) {
   constexpr int SU = CSRSPMM_SEG_UNROLL;
   const int nv = p.N / 4;
   const int G = nv >= 64 ? 64 : (pow2_ceil(nv) < 4 ? 4 : pow2_ceil(nv));
-  if constexpr (!LDS && BUF) {
+  if constexpr (BUF) {
     const long long mean4 = p.M > 0 ? 4LL * p.nnz / p.M : 0;
     if ((G == 16 || G == 32) && p.dp.P == 0 && p.row_hint >= 0 &&
         p.row_hint <= std::max<long long>(p.long_row, mean4) &&
@@ -1098,8 +1116,8 @@ static hipError_t dispatch_vec4_cols(const Problem& p, hipStream_t s) {
       Problem q = p;
       sweep_geometry(p.K, G * 4, q.sweep_shift, q.sweep_bands);
       if (q.sweep_bands >= 2) {
-        if (G == 16) return launch_rg<4, 16, 1, kVec4U, false, CSRSPMM_SWEEP_SU, true, true>(q, s);
-        return launch_rg<4, 32, 1, kVec4U, false, CSRSPMM_SWEEP_SU, true, true>(q, s);
+        if (G == 16) return launch_rg<4, 16, 1, kVec4U, LDS, CSRSPMM_SWEEP_SU, true, true>(q, s);
+        return launch_rg<4, 32, 1, kVec4U, LDS, CSRSPMM_SWEEP_SU, true, true>(q, s);
       }
     }
   }
@@ -1147,12 +1165,12 @@ static hipError_t dispatch_vec4(const Problem& p, hipStream_t s) {
   // configs within 1%.  Unsliced 16-lane calls keep 4 (XL at N = 64 lost 7%).
   static_assert(kSliceWidth == 64, "a slice's float4 chunks fill 16-lane groups");
   if (p.sw == kSliceWidth) {
-    // The register variant sweeps the short rows of each slice band by band
-    // (sweep_rows); the LDS-staged variant keeps the merge blocks.
-    if (!LDS && sweep_applies(p.plan, p.M, p.K, p.nnz, p.sw) && buf_gathers_ok(p)) {
+    // The short rows of each slice are swept band by band (sweep_rows); the
+    // LDS-staged variant passes each chunk through its stage.
+    if (sweep_applies(p.plan, p.M, p.K, p.nnz, p.sw) && buf_gathers_ok(p)) {
       Problem q = p;
       sweep_geometry(p.K, p.sw, q.sweep_shift, q.sweep_bands);
-      return launch_rg<4, 16, 1, kVec4U, false, CSRSPMM_SWEEP_SU, true, true>(q, s);
+      return launch_rg<4, 16, 1, kVec4U, LDS, CSRSPMM_SWEEP_SU, true, true>(q, s);
     }
     return launch_rg<4, 16, 1, kVec4U, LDS, 8>(p, s);
   }

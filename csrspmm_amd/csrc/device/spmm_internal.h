@@ -407,11 +407,11 @@ inline bool sweep_applies(bool plan, int M, int K, int nnz, int sw,
   sweep_geometry(K, sw, shift, bands);
   return (long long)nnz >= (long long)min_per_band * bands * M;
 }
-// The call's slices would be swept (float4 columns, vec 4, of the register
-// variant, with a plan) with at least kSweepWideMinPerBand nonzeros per band
-// and row: slice_width's `sweeps`.
-inline bool wide_sweep(int vec, bool lds, bool plan, int M, int K, int nnz) {
-  return vec == 4 && !lds && sweep_applies(plan, M, K, nnz, kSliceWidth, kSweepWideMinPerBand);
+// The call's slices would be swept (float4 columns, vec 4, with a plan) with
+// at least kSweepWideMinPerBand nonzeros per band and row: slice_width's
+// `sweeps`.
+inline bool wide_sweep(int vec, bool plan, int M, int K, int nnz) {
+  return vec == 4 && sweep_applies(plan, M, K, nnz, kSliceWidth, kSweepWideMinPerBand);
 }
 
 // Segments of a row of len nonzeros under the problem's geometry and hint.

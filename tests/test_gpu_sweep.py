@@ -1,14 +1,14 @@
-"""The band sweep of column slices (rowgroup.hip sweep_rows): float4 calls of
-the register variant whose B is sliced (B of at least 32 MiB, N >= 128, a
-64-column band of at most 16 MiB), whose rows average at least two
-nonzeros per band and which have enough rows for 8192 waves (M >= 65536)
-keep two rows' accumulators per 16-lane group while all groups walk B in
-bands.  Every shape below meets those conditions (K = 32768 or 49152, bands
-of 16384 B rows).  Each case is checked against
-the oracle on every row, and against the LDS-staged variant
-(WarpPerRowSmemFp4), which keeps the merge blocks: both sum every short row
-whole in CSR order and the long rows in the same segments, so the two must
-agree bit for bit.
+"""The band sweep of column slices (rowgroup.hip sweep_rows): float4 calls
+whose B is sliced (B of at least 32 MiB, N >= 128, a 64-column band of at
+most 16 MiB), whose rows average at least two nonzeros per band and which
+have enough rows for 8192 waves (M >= 65536) keep two rows' accumulators
+per 16-lane group while all groups walk B in bands.  Every shape below meets
+those conditions (K = 32768 or 49152, bands of 16384 B rows).  Each case is
+checked against the oracle on every row, against the scalar-column variant
+(WarpPerRow), which keeps the merge blocks, and against the LDS-staged
+float4 variant (WarpPerRowSmemFp4), which sweeps through its LDS stage: all
+sum every short row whole in CSR order and the long rows in the same
+segments, so they must agree bit for bit.
 
 Covered: ragged rows with empty ones, rows above the long-row limit (summed
 by segments, skipped by the sweep), rows with unsorted columns (all of a row
@@ -90,8 +90,10 @@ def test_sweep_against_oracle_and_merge_blocks(case, gpu):
     alpha, beta = 1.5, -0.5
     sweep = run("WarpPerRowFp4", gpu, rp, ci, va, B, C0, alpha, beta)
     check_all(sweep.cpu().numpy(), rp, ci, va, B, alpha, beta, C0, f"{case} sweep")
-    merge = run("WarpPerRowSmemFp4", gpu, rp, ci, va, B, C0, alpha, beta)
+    merge = run("WarpPerRow", gpu, rp, ci, va, B, C0, alpha, beta)
     assert torch.equal(sweep, merge), f"{case}: sweep and merge blocks differ"
+    lds = run("WarpPerRowSmemFp4", gpu, rp, ci, va, B, C0, alpha, beta)
+    assert torch.equal(sweep, lds), f"{case}: the LDS-staged sweep differs"
     auto = run("Auto", gpu, rp, ci, va, B, C0, alpha, beta)
     assert torch.equal(sweep, auto), f"{case}: Auto differs from WarpPerRowFp4"
 
@@ -109,8 +111,8 @@ def test_sweep_with_hints(hint, gpu):
     h = int(np.diff(rp).max()) if hint == "exact" else 90
     C = run("WarpPerRowFp4", gpu, rp, ci, va, B, C0, 1.0, 0.0, hint=h)
     check_all(C.cpu().numpy(), rp, ci, va, B, 1.0, 0.0, None, f"hint {hint}")
-    ref = run("WarpPerRowSmemFp4", gpu, rp, ci, va, B, C0, 1.0, 0.0, hint=h)
-    assert torch.equal(C, ref)
+    for other in ("WarpPerRow", "WarpPerRowSmemFp4"):
+        assert torch.equal(C, run(other, gpu, rp, ci, va, B, C0, 1.0, 0.0, hint=h)), other
 
 
 def test_sweep_strided_operands(gpu):
@@ -155,8 +157,8 @@ def test_sweep_wide_band_with_hint(gpu):
     """A 64-column band wider than 16 MiB (K = 81920: 20 MiB) is sliced only
     when the call sweeps with at least 4 nonzeros per band and no column
     panels can apply, as with a max_row_nnz hint below 1024.  Checked against
-    the oracle and, bit for bit, against the LDS-staged variant, which stays
-    unsliced there."""
+    the oracle and, bit for bit, against the scalar-column variant, which
+    stays unsliced there, and the LDS-staged float4 variant, which sweeps."""
     M, K, N = MS, 81920, 256
     rp, ci, va = rows_csr(lengths_for(M, 18, ((3, 300), (MS - 1, 700))), K, 19, (8,))
     rng = np.random.default_rng(20)
@@ -165,8 +167,8 @@ def test_sweep_wide_band_with_hint(gpu):
     h = int(np.diff(rp).max())
     C = run("WarpPerRowFp4", gpu, rp, ci, va, B, C0, -1.25, 0.5, hint=h)
     check_all(C.cpu().numpy(), rp, ci, va, B, -1.25, 0.5, C0, "wide band")
-    ref = run("WarpPerRowSmemFp4", gpu, rp, ci, va, B, C0, -1.25, 0.5, hint=h)
-    assert torch.equal(C, ref)
+    for other in ("WarpPerRow", "WarpPerRowSmemFp4"):
+        assert torch.equal(C, run(other, gpu, rp, ci, va, B, C0, -1.25, 0.5, hint=h)), other
 
 
 @pytest.mark.parametrize("N", [128, 64])
@@ -178,7 +180,8 @@ def test_unsliced_sweep_with_hint(N, gpu):
     K = 32768 gives a 16 MiB (N = 128) or 8 MiB (N = 64) B in 4 MiB bands.
     Rows of 50-149 nonzeros with one of 300 (segments, skipped by the sweep;
     the hint 300 is below 4x the mean) and one unsorted.  Against the oracle
-    and bit for bit against the merge blocks."""
+    and bit for bit against the merge blocks (WarpPerRow) and the LDS-staged
+    sweep."""
     M, K = (16384 if N == 128 else MS), 32768  # 4096 / 8192 waves
     rng = np.random.default_rng(22)
     lens = rng.integers(50, 150, M)
@@ -189,8 +192,8 @@ def test_unsliced_sweep_with_hint(N, gpu):
     h = int(np.diff(rp).max())
     C = run("WarpPerRowFp4", gpu, rp, ci, va, B, C0, 0.5, -2.0, hint=h)
     check_all(C.cpu().numpy(), rp, ci, va, B, 0.5, -2.0, C0, f"unsliced N={N}")
-    ref = run("WarpPerRowSmemFp4", gpu, rp, ci, va, B, C0, 0.5, -2.0, hint=h)
-    assert torch.equal(C, ref)
+    for other in ("WarpPerRow", "WarpPerRowSmemFp4"):
+        assert torch.equal(C, run(other, gpu, rp, ci, va, B, C0, 0.5, -2.0, hint=h)), other
     no_hint = run("WarpPerRowFp4", gpu, rp, ci, va, B, C0, 0.5, -2.0)
     assert torch.equal(C, no_hint)
 
@@ -200,8 +203,8 @@ def test_unsliced_sweep_with_hint(N, gpu):
 def test_sweep_random_shapes(seed, M, K, N, gpu):
     """Seeded shapes off the powers of two (rows and slices that do not
     divide evenly, a last slice of 4 columns at N = 132), with a few long
-    and unsorted rows: bit for bit against the merge blocks, and against the
-    oracle on sampled rows."""
+    and unsorted rows: bit for bit against the merge blocks (WarpPerRow) and
+    the LDS-staged sweep, and against the oracle on sampled rows."""
     rng = np.random.default_rng(seed)
     lens = rng.integers(0, 2 * (seed % 5 + 20), M)
     for r in rng.choice(M, 6, replace=False):
@@ -210,8 +213,8 @@ def test_sweep_random_shapes(seed, M, K, N, gpu):
     B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
     C0 = rng.uniform(-1, 1, (M, N)).astype(np.float32)
     C = run("WarpPerRowFp4", gpu, rp, ci, va, B, C0, 1.0, 1.0)
-    ref = run("WarpPerRowSmemFp4", gpu, rp, ci, va, B, C0, 1.0, 1.0)
-    assert torch.equal(C, ref)
+    for other in ("WarpPerRow", "WarpPerRowSmemFp4"):
+        assert torch.equal(C, run(other, gpu, rp, ci, va, B, C0, 1.0, 1.0)), other
     rows = np.unique(np.concatenate([rng.choice(M, 3000, replace=False), np.nonzero(lens > 128)[0]]))
     R, S = oracle.spmm_f64(rp, ci, va, B, C0, 1.0, 1.0, rows=rows)
     bad, ratio, _, _ = oracle.check(C.cpu().numpy()[rows], R, S, 1e-5)
