@@ -219,7 +219,24 @@ int owned_workspace_locked(void* stream, size_t bytes, void** out) {
 
 }  // namespace
 
+// A float4 call from N = 128 whose column slices would be swept (the plan,
+// slice_width and sweep_applies as spmm_impl and the dispatch decide them).
+static bool sliced_sweep(int M, int K, int N, int nnz, int hint) {
+  const bool plan = wants_plan(CSRSPMM_ALGO_WARP_PER_ROW_FP4, M, nnz, hint);
+  if (!plan) return false;
+  const int P = per_call_panels(4, plan, K, N, nnz, hint);
+  return slice_width(K, N, P > 0, wide_sweep(4, plan, M, K, nnz)) > 0 &&
+         sweep_applies(plan, M, K, nnz, kSliceWidth);
+}
+
 int resolve_algorithm(int algo, int M, int K, int N, int nnz, int hint) {
+  if (algo == CSRSPMM_ALGO_AUTO && N % 4 == 0 && N >= 128 && sliced_sweep(M, K, N, nnz, hint)) {
+    // Swept column slices run 0-5% faster with the chunks through LDS than
+    // broadcast across lanes.  Measured on MI355X per call: large 299 ->
+    // 286 us, 65536^2 x 256 with 128 per row 490 -> 465, 65536^2 x 512 with
+    // 66 per row 591 -> 564; 16 per row and power-law rows within 0.4%.
+    return CSRSPMM_ALGO_WARP_PER_ROW_SMEM_FP4;
+  }
   if (algo == CSRSPMM_ALGO_AUTO && N % 4 == 0 && N < 128 && (long long)nnz >= 24LL * M &&
       per_call_panels(4, wants_plan(CSRSPMM_ALGO_WARP_PER_ROW_FP4, M, nnz, hint), K, N, nnz, hint) > 0) {
     // Below N = 128 the float4 form has the per-call column panels from a

@@ -72,6 +72,11 @@ def test_parse_and_names():
     assert ex(6, 1 << 20, 1 << 20, 64, 16 << 20) == 4       # R-MAT-like: 16 per row
     assert ex(6, 262144, 262144, 66, 8453223) == 4          # N % 4 != 0
     assert ex(6, 4096, 4096, 64, 4096 * 200) == 4           # small B: scalar
+    # from N = 128, swept column slices take the float4 LDS-staged variant
+    assert ex(6, 65536, 65536, 256, 4325376) == 5           # large
+    assert ex(6, 65536, 65536, 256, 65536 * 7) == 3         # under 2 per band: merge blocks
+    assert ex(6, 32768, 65536, 256, 4325376) == 3           # too few rows to sweep
+    assert ex(6, 1 << 20, 1 << 20, 512, 16 << 20) == 3      # R-MAT N = 512: 0.25 per band
     assert ex(3, 4096, 4096, 128, 4096 * 200) == 3          # concrete ids pass through
     assert ex(9, 4096, 4096, 128, 4096 * 200) == -1
     assert lib.csrspmm_version() >= 100

@@ -28,7 +28,10 @@ def test_plan_configs(cfg_name, algo, gpu):
     rp, ci, va = dev_t(a.rowptr, gpu), dev_t(a.colidx, gpu), dev_t(a.vals, gpu)
     plan = capi.Plan(algo, rp, ci, va, a.K, n_hint=cfg.N)
     if algo == "Auto":
-        assert plan.algorithm == ("WarpPerRowFp4" if cfg.N >= 128 else "WarpPerRowSmem")
+        ex = capi.hip().csrspmm_resolve_algorithm_ex(capi.ALGO["Auto"], a.M, a.K, cfg.N, a.nnz,
+                                                     int(np.diff(a.rowptr).max()))
+        assert plan.algorithm == capi.hip().csrspmm_algorithm_name(ex).decode()
+        assert plan.algorithm in ("WarpPerRowFp4", "WarpPerRowSmemFp4", "WarpPerRowSmem")
     rows = sample_rows(a, cfg_name in ("host", "medium"))
     concrete = plan.algorithm
     C1 = plan_run(plan, B, gpu, a.M, cfg.N)
