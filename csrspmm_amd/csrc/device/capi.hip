@@ -107,9 +107,11 @@ bool is_rowgroup(int algo) {
 }
 
 // The plan pays for itself on large matrices (short rows are streamed,
-// long rows split); small ones with no row above kSegLen run as one launch.
-bool wants_plan(int algo, int M, int nnz, int hint) {
+// long rows split); small ones with no row above kSegLen run as one launch,
+// and so do mid-sized ones whose hint rules out long rows (plan_skips).
+bool wants_plan(int algo, int M, int K, int N, int nnz, int hint) {
   if (!is_rowgroup(algo)) return false;
+  if (plan_skips(M, K, N, nnz, hint)) return false;
   if ((long long)M + nnz >= kPlanMinItems) return true;
   return (hint < 0 || hint > kSegLen) && nnz > kSegLen;
 }
@@ -222,7 +224,7 @@ int owned_workspace_locked(void* stream, size_t bytes, void** out) {
 // A float4 call from N = 128 whose column slices would be swept (the plan,
 // slice_width and sweep_applies as spmm_impl and the dispatch decide them).
 static bool sliced_sweep(int M, int K, int N, int nnz, int hint) {
-  const bool plan = wants_plan(CSRSPMM_ALGO_WARP_PER_ROW_FP4, M, nnz, hint);
+  const bool plan = wants_plan(CSRSPMM_ALGO_WARP_PER_ROW_FP4, M, K, N, nnz, hint);
   if (!plan) return false;
   const int P = per_call_panels(4, plan, K, N, nnz, hint);
   return slice_width(K, N, P > 0, wide_sweep(4, plan, M, K, nnz)) > 0 &&
@@ -238,7 +240,7 @@ int resolve_algorithm(int algo, int M, int K, int N, int nnz, int hint) {
     return CSRSPMM_ALGO_WARP_PER_ROW_SMEM_FP4;
   }
   if (algo == CSRSPMM_ALGO_AUTO && N % 4 == 0 && N < 128 && (long long)nnz >= 24LL * M &&
-      per_call_panels(4, wants_plan(CSRSPMM_ALGO_WARP_PER_ROW_FP4, M, nnz, hint), K, N, nnz, hint) > 0) {
+      per_call_panels(4, wants_plan(CSRSPMM_ALGO_WARP_PER_ROW_FP4, M, K, N, nnz, hint), K, N, nnz, hint) > 0) {
     // Below N = 128 the float4 form has the per-call column panels from a
     // 64 MiB B, the scalar form none.  Measured on MI355X per call with the
     // hint: power-law rows at K = 262144 (mean 32) N = 64 320.5 -> 227.4 us,
@@ -387,7 +389,7 @@ int spmm_impl(int algo_in, int M, int K, int N, int nnz, const int* rowptr, cons
   hipStream_t s = static_cast<hipStream_t>(stream);
   // held (owned workspaces only) until the kernels are enqueued
   std::unique_lock<std::mutex> lock;
-  p.plan = wants_plan(algo, M, nnz, hint);
+  p.plan = wants_plan(algo, M, K, N, nnz, hint);
   if (p.plan) {
     const int vec = vector_width(algo, p);
     int P = per_call_panels(vec, true, K, N, nnz, hint);
@@ -555,7 +557,7 @@ int csrspmm_resolve_algorithm_ex(int algo, int M, int K, int N, int nnz, int max
 
 size_t csrspmm_workspace_bytes(int algo, int M, int N, int nnz) {
   algo = resolve_algorithm(algo, N);
-  if (M <= 0 || N <= 0 || nnz < 0 || !wants_plan(algo, M, nnz, -1)) return 0;
+  if (M <= 0 || N <= 0 || nnz < 0 || !wants_plan(algo, M, 0, N, nnz, -1)) return 0;
   return workspace_layout(M, 0, N, nnz, 0).base_total;
 }
 
@@ -563,7 +565,7 @@ size_t csrspmm_workspace_bytes(int algo, int M, int N, int nnz) {
 // alignment is checked per call); -1 when the call makes no plan.
 static int shape_panels(int algo, int M, int K, int N, int nnz, int hint) {
   algo = resolve_algorithm(algo, M, K, N, nnz, hint);
-  if (M <= 0 || N <= 0 || nnz < 0 || K < 0 || !wants_plan(algo, M, nnz, hint)) return -1;
+  if (M <= 0 || N <= 0 || nnz < 0 || K < 0 || !wants_plan(algo, M, K, N, nnz, hint)) return -1;
   const bool fp4 = (algo == CSRSPMM_ALGO_WARP_PER_ROW_FP4 || algo == CSRSPMM_ALGO_WARP_PER_ROW_SMEM_FP4) &&
                    N % 4 == 0;
   int P = per_call_panels(fp4 ? 4 : 1, true, K, N, nnz, hint);

@@ -132,6 +132,26 @@ inline int merge_blocks(int M, int nnz, int mblk) {
 // Below this many (rows + nonzeros) the plan is skipped and each row is
 // processed whole by one group (one launch instead of three).
 constexpr long long kPlanMinItems = 1 << 16;
+// With a max_row_nnz hint of at most kPlanSkipMaxRow, a problem of fewer
+// than kPlanSkipItems (rows + nonzeros) and kPlanSkipRows rows, without
+// column slices, runs as one launch too (plan_skips): one group per row,
+// every row summed whole.  The plan's and the combine's launches cost more
+// than the merge blocks and the split rows save.  Measured on MI355X per
+// call (Auto, the hint = the longest row): 4096^2 x 128 with 41 per row
+// 14.4 -> 9.8 us, 8192 x 4096 x 256 with 41 per row 22.0 -> 17.4 us,
+// 16384^2 x 128 with 20 per row 19.4 -> 16.6 us, 16384^2 x 256 with 60 per
+// row 105 -> 95 us, 8192 x 131072 x 128 with 100 per row 58.4 -> 46.8 us;
+// rows of 129-256 (which the plan cuts into segments of 32 on a small
+// matrix): 1024 x 2048 x 128 with 200 per row 19.2 -> 13.0 us, 4096^2 x 128
+// with 200 per row 24.6 -> 18.8 us, 2048 x 131072 x 128 with 250 per row
+// 44.6 -> 34.4 us, 3072 x 262144 x 256 with 200 per row 87.9 -> 79.7 us.
+// From 32768 rows the band sweep, which needs the plan, leads (32768^2 x
+// 128 with 20 per row 31.3 us planned against 39.5 us, 65536^2 x 128 with
+// 12 per row 49.1 against 56.5 us), and sliced calls keep it too (16384^2 x
+// 512 with 50 per row 192 against 201 us).
+constexpr long long kPlanSkipItems = 1 << 20;
+constexpr int kPlanSkipRows = 32768;
+constexpr int kPlanSkipMaxRow = 256;
 
 // XCDs of an MI355X.  Workgroups are dispatched to them round-robin by
 // workgroup id, which stored plans use for L2 locality (plan.hip).
@@ -230,6 +250,12 @@ inline int slice_width(int K, int N, bool panels, bool sweeps = false) {
   const bool wide = CSRSPMM_SWEEP_WIDE && sweeps && !panels;
   if (band > ((long long)CSRSPMM_SLICE_BAND_MAX_MB << 20) && full < (1LL << 30) && !wide) return 0;
   return kSliceWidth;
+}
+
+// The plan is skipped for a hinted short-row problem (kPlanSkipItems).
+inline bool plan_skips(int M, int K, int N, int nnz, int hint) {
+  return hint >= 0 && hint <= kPlanSkipMaxRow && M < kPlanSkipRows &&
+         (long long)M + nnz < kPlanSkipItems && slice_width(K, N, false) == 0;
 }
 
 // Resident blocks per CU for slices launched one by one over a band wider

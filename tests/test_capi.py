@@ -131,6 +131,25 @@ def test_workspace_bytes():
     assert lib.csrspmm_workspace_bytes(3, 10, 16, 20) == 0  # tiny, no long row possible
 
 
+def test_hinted_short_rows_skip_the_plan():
+    """A hint of at most 256 nonzeros per row on fewer than 2^20 rows +
+    nonzeros and 32768 rows, with no column slices, runs as one launch: no
+    workspace.  Without the hint, with a longer row possible, from 32768 rows
+    (the band sweep needs the plan) or with slices, the plan stays."""
+    lib = capi.hip()
+    ex = lib.csrspmm_workspace_bytes_ex
+    for algo in ("Auto", "WarpPerRow", "WarpPerRowFp4", "WarpPerRowSmem", "WarpPerRowSmemFp4"):
+        a = capi.ALGO[algo]
+        assert ex(a, 4096, 4096, 128, 4096 * 41, 60) == 0
+        assert ex(a, 4096, 4096, 128, 4096 * 41, 256) == 0
+        assert ex(a, 4096, 4096, 128, 4096 * 41, -1) > 0      # no hint
+        assert ex(a, 4096, 4096, 128, 4096 * 41, 257) > 0     # a row of 257 possible
+        assert ex(a, 16384, 16384, 256, 16384 * 60, 70) == 0  # 999,424 items
+        assert ex(a, 16384, 16384, 256, 16384 * 63, 70) > 0   # 2^20 items or more
+        assert ex(a, 32768, 32768, 128, 32768 * 20, 30) > 0   # 32768 rows
+        assert ex(a, 16384, 16384, 512, 16384 * 50, 60) > 0   # 64-column slices
+
+
 def test_ex_rejects_small_workspace_without_device():
     lib = capi.hip()
     fake = 0x1000

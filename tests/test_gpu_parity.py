@@ -24,7 +24,7 @@ import torch
 
 import oracle
 from csrspmm_amd import ALGORITHMS, capi, configs, gen
-from csr_cases import whole_row_max
+from csr_cases import csr_from_lengths, whole_row_max
 from golden_cases import load, names
 
 pytestmark = pytest.mark.gpu
@@ -212,6 +212,40 @@ def test_row_hint(algo, hint, gpu):
     C0 = rng.uniform(-1, 1, (lens.size, 64)).astype(np.float32)
     C = run_spmm(algo, rowptr, colidx, vals, B, gpu, C0=C0, alpha=0.5, beta=2.0, hint=hint)
     assert_parity(algo, C, rowptr, colidx, vals, B, C0, 0.5, 2.0, what=f"hint={hint} beta")
+
+
+@functools.lru_cache(maxsize=None)
+def short_row_problem(shape):
+    M, K, per, N = shape
+    rng = np.random.default_rng(M + per)
+    lens = rng.integers(per // 2, per + per // 2 + 1, M)
+    lens[::97] = 0
+    rowptr, colidx, vals = csr_from_lengths(lens, K, seed=M + per)
+    B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+    C0 = rng.uniform(-1, 1, (M, N)).astype(np.float32)
+    return lens, rowptr, colidx, vals, B, C0
+
+
+@pytest.mark.parametrize("algo", ["Auto", "WarpPerRow", "WarpPerRowFp4", "WarpPerRowSmem", "WarpPerRowSmemFp4"])
+@pytest.mark.parametrize("shape", [(4096, 4096, 41, 128), (16384, 16384, 60, 256), (8192, 4096, 41, 96),
+                                   (2048, 4096, 150, 256)])
+def test_hinted_short_rows_one_launch(algo, shape, gpu):
+    """A hint of at most 256 on a mid-sized problem (under 2^20 rows +
+    nonzeros and 32768 rows, no column slices) skips the plan: one group per
+    row, one launch, no workspace.  Every row against the oracle and bit for
+    bit against the fp32 restatement, every row being summed whole, with the
+    hint at the longest row and at 256, and with beta != 0."""
+    M, K, per, N = shape
+    lens, rowptr, colidx, vals, B, C0 = short_row_problem(shape)
+    for hint in (int(lens.max()), 256):
+        assert capi.hip().csrspmm_workspace_bytes_ex(capi.ALGO[algo], M, K, N, colidx.size, hint) == 0
+        print(f"[parity] one launch {algo} M={M} K={K} N={N} hint={hint}", flush=True)
+        C = run_spmm(algo, rowptr, colidx, vals, B, gpu, hint=hint)
+        assert_parity(algo, C, rowptr, colidx, vals, B, None, 1.0, 0.0, what=f"hint={hint}")
+        F = oracle.spmm_f32_seq(rowptr, colidx, vals, B, None, 1.0, 0.0)
+        assert np.array_equal(C.view(np.uint32), F.view(np.uint32)), "rows summed whole"
+    C = run_spmm(algo, rowptr, colidx, vals, B, gpu, C0=C0, alpha=0.5, beta=-1.5, hint=int(lens.max()))
+    assert_parity(algo, C, rowptr, colidx, vals, B, C0, 0.5, -1.5, what="beta")
 
 
 @pytest.mark.parametrize("algo", ALGORITHMS)
