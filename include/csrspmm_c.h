@@ -108,7 +108,10 @@ size_t csrspmm_workspace_bytes(int algo, int M, int N, int nnz);
  * ones (at most 256 MiB of partials).  A
  * max_row_nnz_hint in [0, 1024) tells that no such row exists (-1: unknown).
  * csrspmm_spmm_f32_ex given a workspace of at least
- * csrspmm_workspace_bytes but less than this size runs without panels. */
+ * csrspmm_workspace_bytes but less than this size runs without panels.
+ * A hint in [0, 256] on fewer than 2^20 rows + nonzeros and 32768 rows, when
+ * B is not cut into column slices, gives 0: such a call runs as one launch
+ * with no plan and no workspace. */
 size_t csrspmm_workspace_bytes_ex(int algo, int M, int K, int N, int nnz, int max_row_nnz_hint);
 
 /* Where a per-call workspace of csrspmm_workspace_bytes_ex bytes holds the
