@@ -129,9 +129,15 @@ Tensor csrspmm_warp_per_row_smem_fp4_forward(Tensor A_row_ptr, Tensor A_col_idx,
                  static_cast<int>(std::min<int64_t>(A_max_row_nnz, INT32_MAX)), B, alpha, beta);
 }
 
+// max_row_nnz: the longest row, or -1 when unknown (a scheduling hint only).
+int row_hint(int64_t max_row_nnz) {
+  return max_row_nnz < 0 ? -1 : static_cast<int>(std::min<int64_t>(max_row_nnz, INT32_MAX));
+}
+
 Tensor csrspmm_auto_forward(Tensor A_row_ptr, Tensor A_col_idx, Tensor A_values, Tensor B,
-                            double alpha, double beta) {
-  return forward(CSRSPMM_ALGO_AUTO, A_row_ptr, A_col_idx, A_values, -1, B, alpha, beta);
+                            double alpha, double beta, int64_t max_row_nnz) {
+  return forward(CSRSPMM_ALGO_AUTO, A_row_ptr, A_col_idx, A_values, row_hint(max_row_nnz), B, alpha,
+                 beta);
 }
 
 int algo_id(const std::string& name) {
@@ -151,7 +157,7 @@ void check_out(const Tensor& C, const Tensor& B, int64_t M) {
 // (the reference's C++ spmm() semantics, src/csrspmm.cpp:28-75; its torch
 // forwards always start from a fresh C).
 Tensor csrspmm_spmm_out(Tensor A_row_ptr, Tensor A_col_idx, Tensor A_values, Tensor B, Tensor C,
-                        double alpha_d, double beta_d, const std::string& algo) {
+                        double alpha_d, double beta_d, const std::string& algo, int64_t max_row_nnz) {
   check_inputs(A_row_ptr, A_col_idx, A_values, B);
   const int M = static_cast<int>(A_row_ptr.size(0) - 1);
   check_out(C, B, M);
@@ -160,13 +166,14 @@ Tensor csrspmm_spmm_out(Tensor A_row_ptr, Tensor A_col_idx, Tensor A_values, Ten
   const int nnz = static_cast<int>(A_values.size(0));
   if (M == 0 || N == 0) return C;
   const int a = algo_id(algo);
-  const size_t ws_bytes = csrspmm_workspace_bytes_ex(a, M, K, N, nnz, -1);
+  const int hint = row_hint(max_row_nnz);
+  const size_t ws_bytes = csrspmm_workspace_bytes_ex(a, M, K, N, nnz, hint);
   Tensor ws;
   if (ws_bytes > 0) ws = torch::empty({static_cast<int64_t>(ws_bytes)}, B.options().dtype(torch::kUInt8));
   hipStream_t stream = c10::hip::getCurrentHIPStream(B.device().index()).stream();
   const int st = csrspmm_spmm_f32_ex(a, M, K, N, nnz, A_row_ptr.data_ptr<int>(),
                                      nnz ? A_col_idx.data_ptr<int>() : nullptr,
-                                     nnz ? A_values.data_ptr<float>() : nullptr, -1,
+                                     nnz ? A_values.data_ptr<float>() : nullptr, hint,
                                      B.numel() ? B.data_ptr<float>() : nullptr, leading_dim(B, "B"),
                                      C.data_ptr<float>(), leading_dim(C, "C"), static_cast<float>(alpha_d),
                                      static_cast<float>(beta_d), 0u,

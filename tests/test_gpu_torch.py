@@ -114,6 +114,34 @@ def test_xl_through_torch(gpu):
     assert bad == 0, ratio
 
 
+def test_auto_and_spmm_out_take_the_row_hint(gpu):
+    """max_row_nnz is a scheduling hint only: given (true, or too low) or not,
+    csrspmm_auto and csrspmm_spmm_out agree with the oracle, and with a hint
+    of at most 256 on a mid-sized matrix (one launch, rows summed whole) bit
+    for bit with the fp32 CSR-order restatement."""
+    from csr_cases import csr_from_lengths
+    rng = np.random.default_rng(12)
+    lens = rng.integers(0, 90, 6000)
+    lens[17] = 400  # longer than the too-low hint below
+    rp, ci, va = csr_from_lengths(lens, 5000, seed=12)
+    t = lambda x: torch.from_numpy(x).to(gpu)  # noqa: E731
+    B = rng.standard_normal((5000, 128)).astype(np.float32)
+    C0 = rng.standard_normal((6000, 128)).astype(np.float32)
+    for mx in (-1, 400, 100):
+        C = tc.csrspmm_auto(t(rp), t(ci), t(va), t(B), 1.0, 0.0, max_row_nnz=mx)
+        R, S = oracle.spmm_f64(rp, ci, va, B, None, 1.0, 0.0)
+        bad, ratio, _, _ = oracle.check(C.cpu().numpy(), R, S, 1e-5)
+        assert bad == 0, f"auto max_row_nnz={mx}: {ratio}"
+        dC = t(C0)
+        tc.csrspmm_spmm_out(t(rp), t(ci), t(va), t(B), dC, 0.5, -1.25, max_row_nnz=mx)
+        R, S = oracle.spmm_f64(rp, ci, va, B, C0, 0.5, -1.25)
+        bad, ratio, _, _ = oracle.check(dC.cpu().numpy(), R, S, 1e-5)
+        assert bad == 0, f"spmm_out max_row_nnz={mx}: {ratio}"
+        if mx == 100:  # at most 256: one launch, every row summed whole
+            F = oracle.spmm_f32_seq(rp, ci, va, B, None, 1.0, 0.0)
+            assert np.array_equal(C.cpu().numpy().view(np.uint32), F.view(np.uint32))
+
+
 def test_auto_and_spmm_out(gpu):
     rng = np.random.default_rng(11)
     rp, ci, va, mx = random_csr(500, 300, 0.1, rng)

@@ -57,15 +57,18 @@ def csrspmm_warp_per_row_smem_fp4(A_rowptr, A_colidx, A_values, A_max_row_nnz, B
                                             beta)
 
 
-def csrspmm_auto(A_rowptr, A_colidx, A_values, B, alpha, beta):
+def csrspmm_auto(A_rowptr, A_colidx, A_values, B, alpha, beta, max_row_nnz=-1):
     """As the five entry points, with the variant picked from the shape
-    (csrspmm_resolve_algorithm_ex)."""
-    return _C.csrspmm_auto(A_rowptr, A_colidx, A_values, B, alpha, beta)
+    (csrspmm_resolve_algorithm_ex).  max_row_nnz, the longest row when known
+    (-1: unknown), is a scheduling hint only: with at most 256 a mid-sized
+    product runs as one launch."""
+    return _C.csrspmm_auto(A_rowptr, A_colidx, A_values, B, alpha, beta, max_row_nnz)
 
 
-def csrspmm_spmm_out(A_rowptr, A_colidx, A_values, B, C, alpha, beta, algo="Auto"):
-    """C = alpha * A @ B + beta * C in place (C is read when beta != 0); returns C."""
-    return _C.csrspmm_spmm_out(A_rowptr, A_colidx, A_values, B, C, alpha, beta, algo)
+def csrspmm_spmm_out(A_rowptr, A_colidx, A_values, B, C, alpha, beta, algo="Auto", max_row_nnz=-1):
+    """C = alpha * A @ B + beta * C in place (C is read when beta != 0); returns C.
+    max_row_nnz as for csrspmm_auto."""
+    return _C.csrspmm_spmm_out(A_rowptr, A_colidx, A_values, B, C, alpha, beta, algo, max_row_nnz)
 
 
 class CsrSpmmPlan:
