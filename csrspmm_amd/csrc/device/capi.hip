@@ -231,7 +231,29 @@ static bool sliced_sweep(int M, int K, int N, int nnz, int hint) {
          sweep_applies(plan, M, K, nnz, kSliceWidth);
 }
 
+// A call from N = 128 that would be cut into column slices (the plan and
+// slice_width as spmm_impl decides them).
+static bool sliced(int M, int K, int N, int nnz, int hint) {
+  const bool plan = wants_plan(CSRSPMM_ALGO_WARP_PER_ROW_FP4, M, K, N, nnz, hint);
+  if (!plan) return false;
+  const int P = per_call_panels(4, plan, K, N, nnz, hint);
+  return slice_width(K, N, P > 0, wide_sweep(4, plan, M, K, nnz)) > 0;
+}
+
 int resolve_algorithm(int algo, int M, int K, int N, int nnz, int hint) {
+  if (algo == CSRSPMM_ALGO_AUTO && N % 4 == 0 && N >= 128 && M > 0 && hint > kLongRow &&
+      (long long)hint > 4LL * nnz / M && sliced(M, K, N, nnz, hint)) {
+    // Column slices of skewed rows (the hint above both long_row and 4x the
+    // mean): the scalar LDS-staged form's 64-lane groups run each slice's
+    // long-row chains with four times the waves of the float4 16-lane
+    // groups.  Measured on MI355X per call with the hint: power-law rows
+    // (mean 32) at K = 65536, N = 256 307 -> 269 us (swept by the float4
+    // form) and K = 32768, N = 512 579 -> 337; mean 98 at K = 131072, N = 512
+    // 3855 -> 3536; R-MAT N = 256 2303 -> 2186, N = 512 4876 -> 4726.
+    // Uniform rows of 200 at K = 65536, N = 256 (the hint within 4x the mean)
+    // keep the float4 sweep: 1248 against 1351 us.
+    return CSRSPMM_ALGO_WARP_PER_ROW_SMEM;
+  }
   if (algo == CSRSPMM_ALGO_AUTO && N % 4 == 0 && N >= 128 && sliced_sweep(M, K, N, nnz, hint)) {
     // Swept column slices run 0-5% faster with the chunks through LDS than
     // broadcast across lanes.  Measured on MI355X per call: large 299 ->

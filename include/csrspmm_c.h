@@ -89,9 +89,12 @@ int csrspmm_resolve_algorithm(int algo, int N);
  *    broadcast variant, which has the panels;
  *  - at N = 128 a B of at most 4 MiB with rows of 160 or more nonzeros on
  *    average (M >= 4096) takes the scalar LDS-staged variant;
- *  - from N = 128, a call whose column slices are swept (a B of at least
- *    32 MiB in bands, rows dense enough per band, M large enough) takes the
- *    float4 LDS-staged variant.
+ *  - from N = 128, a call cut into column slices whose hint exceeds both
+ *    128 and 4x the mean row length (skewed rows) takes the scalar
+ *    LDS-staged variant;
+ *  - otherwise, from N = 128, a call whose column slices are swept (a B of
+ *    at least 32 MiB in bands, rows dense enough per band, M large enough)
+ *    takes the float4 LDS-staged variant.
  * The SpMM entry points resolve Auto this way, and stored plans with the
  * true longest row.  No counterpart in the reference, whose Auto stub is
  * empty. */

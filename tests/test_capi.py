@@ -77,6 +77,12 @@ def test_parse_and_names():
     assert ex(6, 65536, 65536, 256, 65536 * 7) == 3         # under 2 per band: merge blocks
     assert ex(6, 32768, 65536, 256, 4325376) == 3           # too few rows to sweep
     assert ex(6, 1 << 20, 1 << 20, 512, 16 << 20) == 3      # R-MAT N = 512: 0.25 per band
+    # sliced calls of skewed rows (a hint above 128 and 4x the mean) take the scalar LDS form
+    assert ex(6, 1 << 20, 1 << 20, 512, 16084813, 39531) == 4   # R-MAT N = 512 with its hint
+    assert ex(6, 65536, 65536, 256, 65536 * 32, 16384) == 4     # power-law rows, even swept
+    assert ex(6, 65536, 65536, 256, 65536 * 200, 250) == 5      # uniform long rows: the sweep
+    assert ex(6, 65536, 65536, 256, 65536 * 32, 128) == 5       # no long row: the sweep
+    assert ex(6, 131072, 131072, 256, 131072 * 32, 16384) == 3  # unsliced (panels): float4
     assert ex(3, 4096, 4096, 128, 4096 * 200) == 3          # concrete ids pass through
     assert ex(9, 4096, 4096, 128, 4096 * 200) == -1
     assert lib.csrspmm_version() >= 100
