@@ -139,11 +139,13 @@ int csrspmm_workspace_panel_info(int algo, int M, int K, int N, int nnz, int max
  *                   per-call path does not check (csrspmm_validate_csr does).
  *                   Columns need not be sorted within a row.
  *   max_row_nnz_hint       -1 if unknown; otherwise the caller's claim of the
- *                   longest row.  It only steers the plan: at most 128 drops
- *                   the long-row segments and their combine pass, below 512
- *                   the split rows and the combine, below 1024 the column
- *                   panels, and a small matrix with no row above 256 runs as
- *                   one launch.  Never used to size memory or bound a loop:
+ *                   longest row.  It only steers the schedule (and Auto's
+ *                   variant): at most 128 drops the long-row segments and
+ *                   their combine pass, below 512 the split rows and the
+ *                   combine, below 1024 the column panels, and a matrix under
+ *                   2^20 rows + nonzeros and 32768 rows (no column slices)
+ *                   with no row above 256 runs as one launch.  Never used to
+ *                   size memory or bound a loop:
  *                   a hint below the true longest row still gives the exact
  *                   result, only more slowly.
  *   B, ldb, C, ldc  row-major dense operands, ldb >= N, ldc >= N
