@@ -261,6 +261,19 @@ int resolve_algorithm(int algo, int M, int K, int N, int nnz, int hint) {
     // 66 per row 591 -> 564; 16 per row and power-law rows within 0.4%.
     return CSRSPMM_ALGO_WARP_PER_ROW_SMEM_FP4;
   }
+  if (algo == CSRSPMM_ALGO_AUTO && N % 4 == 0 && N >= 128 && hint > kLongRow && hint < 2 * kSegLen &&
+      sliced(M, K, N, nnz, hint)) {
+    // Column slices that do not sweep, of rows up to 511 nonzeros, above
+    // long_row: each such row is one chain of gathers per slice, and the
+    // float4 16-lane groups (four per wave) leave few waves when rows are
+    // few.  Measured on MI355X per call with the hint, uniform rows,
+    // bit-identical: 4096^2 x 2048 with 300 per row 1368 -> 607 us, 2048 x
+    // 16384 x 1024 with 400 per row 388 -> 275, 8192 x 16384 x 512 with 300
+    // per row 464 -> 312, 4096 x 32768 x 256 with 150 per row 102 -> 58,
+    // 16384^2 x 512 with 200 per row 497 -> 402; 2048 x 65536 x 256 with 500
+    // per row 126 against 132 us.
+    return CSRSPMM_ALGO_WARP_PER_ROW_SMEM;
+  }
   if (algo == CSRSPMM_ALGO_AUTO && N % 4 == 0 && N < 128 && (long long)nnz >= 24LL * M &&
       per_call_panels(4, wants_plan(CSRSPMM_ALGO_WARP_PER_ROW_FP4, M, K, N, nnz, hint), K, N, nnz, hint) > 0) {
     // Below N = 128 the float4 form has the per-call column panels from a

@@ -94,7 +94,9 @@ int csrspmm_resolve_algorithm(int algo, int N);
  *    LDS-staged variant;
  *  - otherwise, from N = 128, a call whose column slices are swept (a B of
  *    at least 32 MiB in bands, rows dense enough per band, M large enough)
- *    takes the float4 LDS-staged variant.
+ *    takes the float4 LDS-staged variant;
+ *  - and a sliced call that is not swept, with a hint of 129 to 511, takes
+ *    the scalar LDS-staged variant.
  * The SpMM entry points resolve Auto this way, and stored plans with the
  * true longest row.  No counterpart in the reference, whose Auto stub is
  * empty. */

@@ -83,6 +83,12 @@ def test_parse_and_names():
     assert ex(6, 65536, 65536, 256, 65536 * 200, 250) == 5      # uniform long rows: the sweep
     assert ex(6, 65536, 65536, 256, 65536 * 32, 128) == 5       # no long row: the sweep
     assert ex(6, 131072, 131072, 256, 131072 * 32, 16384) == 3  # unsliced (panels): float4
+    # sliced calls that do not sweep, of rows of 129..511 nonzeros, take it too
+    assert ex(6, 4096, 4096, 2048, 4096 * 300, 300) == 4
+    assert ex(6, 8192, 16384, 512, 8192 * 300, 300) == 4
+    assert ex(6, 8192, 16384, 512, 8192 * 300, 128) == 3       # no long row
+    assert ex(6, 8192, 16384, 512, 8192 * 300, 512) == 3       # rows split into segments
+    assert ex(6, 8192, 16384, 512, 8192 * 300, -1) == 3        # no hint
     assert ex(3, 4096, 4096, 128, 4096 * 200) == 3          # concrete ids pass through
     assert ex(9, 4096, 4096, 128, 4096 * 200) == -1
     assert lib.csrspmm_version() >= 100
