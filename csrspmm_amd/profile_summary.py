@@ -59,8 +59,10 @@ def _run_info(log_path):
     M, nnz, N, balg, bmin, U = map(int, m.groups()[2:8])
     mode = "plan" if "[profile_run] plan " in log else ("nopanels" if "no column panels" in log
                                                          else "")
+    # a stored plan resolves Auto with the matrix's true longest row
+    pm = re.search(r"\[profile_run\] plan (\w+):", log)
     return dict(cfg=cfg, algo=algo, M=M, nnz=nnz, N=N, balg=balg, bmin=bmin, U=U,
-                digest=m.group(9), mode=mode)
+                digest=m.group(9), mode=mode, plan_algo=pm.group(1) if pm else None)
 
 
 def _command(name, info, kind):
@@ -109,7 +111,7 @@ def summarize(prof: str, name: str):
     from . import capi
 
     lib = capi.hip()
-    resolved = lib.csrspmm_algorithm_name(lib.csrspmm_resolve_algorithm_ex(
+    resolved = info["plan_algo"] or lib.csrspmm_algorithm_name(lib.csrspmm_resolve_algorithm_ex(
         capi.ALGO[info["algo"]], info["M"], cfg.K(), info["N"], info["nnz"], -1)).decode()
     what = {"plan": "stored plan, ", "nopanels": "no column panels (base-size workspace), "}.get(
         info["mode"], "")
