@@ -284,7 +284,8 @@ int resolve_algorithm(int algo, int M, int K, int N, int nnz, int hint) {
     // at N = 64.
     return CSRSPMM_ALGO_WARP_PER_ROW_FP4;
   }
-  if (algo == CSRSPMM_ALGO_AUTO && N % 4 == 0 && N == 128 && M >= 4096 &&
+  if (algo == CSRSPMM_ALGO_AUTO && N % 4 == 0 && N == 128 &&
+      (M >= 4096 || (M >= 1024 && plan_skips(M, K, N, nnz, hint))) &&
       (long long)K * N * 4 <= (4LL << 20) && (long long)nnz >= 160LL * M) {
     // A B that stays in the L2s and rows of 160 nonzeros or more on average:
     // the rows are long-row segments, and the scalar LDS-staged form keeps
@@ -292,7 +293,11 @@ int resolve_algorithm(int algo, int M, int K, int N, int nnz, int hint) {
     // rows at N = 128 with max_row_nnz given: M = 4096, K = 4096, 205 per row
     // 33.2 -> 23.0 us, 600 per row 81.8 -> 66.8; M = 16384, K = 2048, 205
     // per row 90.7 -> 68.8; but 64 per row, M = 1024, an 8 MiB B (K = 16384)
-    // or N = 256 keep float4 within 0-21%.
+    // or N = 256 keep float4 within 0-21%.  From M = 1024 when the hint runs
+    // the call as one launch (plan_skips), rows summed whole by one group
+    // each: M = 1024, K = 2048, 200 per row 13.0 -> 10.5 us; M = 1536, K =
+    // 8192, 220 per row 23.1 -> 16.4; M = 2048, K = 2048, 200 per row 13.6 ->
+    // 11.2; M = 1024, K = 1024, 160 per row 10.9 -> 10.0.
     return CSRSPMM_ALGO_WARP_PER_ROW_SMEM;
   }
   return resolve_algorithm(algo, N);

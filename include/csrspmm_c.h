@@ -88,7 +88,8 @@ int csrspmm_resolve_algorithm(int algo, int N);
  *    least 64 MiB, a row of 1024 or more not ruled out) take the float4
  *    broadcast variant, which has the panels;
  *  - at N = 128 a B of at most 4 MiB with rows of 160 or more nonzeros on
- *    average (M >= 4096) takes the scalar LDS-staged variant;
+ *    average (M >= 4096, or M >= 1024 when the hint lets the call run as
+ *    one launch) takes the scalar LDS-staged variant;
  *  - from N = 128, a call cut into column slices whose hint exceeds both
  *    128 and 4x the mean row length (skewed rows) takes the scalar
  *    LDS-staged variant;

@@ -59,6 +59,9 @@ def test_parse_and_names():
     assert ex(6, 4096, 8193, 128, 4096 * 160) == 3          # B above 4 MiB
     assert ex(6, 4096, 4096, 128, 4096 * 160 - 1) == 3      # rows shorter
     assert ex(6, 4095, 4096, 128, 4095 * 200) == 3          # fewer rows
+    assert ex(6, 1024, 2048, 128, 1024 * 200, 250) == 4     # one launch under the hint: from 1024 rows
+    assert ex(6, 1023, 2048, 128, 1023 * 200, 250) == 3
+    assert ex(6, 1024, 2048, 128, 1024 * 200, 257) == 3     # a longer row: the plan
     assert ex(6, 4096, 4096, 256, 4096 * 200) == 3          # N = 256
     assert ex(6, 262144, 262144, 128, 8453223) == 3         # XL
     # below N = 128: float4 when its column panels are possible (B >= 64 MiB,
