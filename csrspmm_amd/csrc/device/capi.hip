@@ -261,18 +261,25 @@ int resolve_algorithm(int algo, int M, int K, int N, int nnz, int hint) {
     // 66 per row 591 -> 564; 16 per row and power-law rows within 0.4%.
     return CSRSPMM_ALGO_WARP_PER_ROW_SMEM_FP4;
   }
-  if (algo == CSRSPMM_ALGO_AUTO && N % 4 == 0 && N >= 128 && hint > kLongRow && hint < 2 * kSegLen &&
-      sliced(M, K, N, nnz, hint)) {
-    // Column slices that do not sweep, of rows up to 511 nonzeros, above
-    // long_row: each such row is one chain of gathers per slice, and the
-    // float4 16-lane groups (four per wave) leave few waves when rows are
-    // few.  Measured on MI355X per call with the hint, uniform rows,
-    // bit-identical: 4096^2 x 2048 with 300 per row 1368 -> 607 us, 2048 x
-    // 16384 x 1024 with 400 per row 388 -> 275, 8192 x 16384 x 512 with 300
-    // per row 464 -> 312, 4096 x 32768 x 256 with 150 per row 102 -> 58,
-    // 16384^2 x 512 with 200 per row 497 -> 402; 2048 x 65536 x 256 with 500
-    // per row 126 against 132 us.
-    return CSRSPMM_ALGO_WARP_PER_ROW_SMEM;
+  if (algo == CSRSPMM_ALGO_AUTO && N % 4 == 0 && N >= 128 && M > 0 && sliced(M, K, N, nnz, hint)) {
+    // Column slices that do not sweep, of rows averaging 64-511 nonzeros or
+    // with the hint at 129-511: a row is one long chain of gathers per
+    // slice, and the scalar 64-lane groups run four times the waves of the
+    // float4 16-lane ones.  Measured on MI355X per call, bit-identical:
+    // uniform rows of 128 at M = 4096, K = 65536, N = 128-1024 1.6-1.9x
+    // faster, of 64 at N = 256 1.3x; at M = K = 32768, N = 256 rows of 128
+    // 357 -> 289 us and of 300 798 -> 632; 4096^2 x 2048 with 300 per row
+    // 1368 -> 607 us, 2048 x 16384 x 1024 with 400 per row 388 -> 275.  On
+    // a 64-column band above kSliceCapBand (8 MiB) the float4 segments, 8
+    // gathers deep under the residency cap, lead as soon as rows exceed
+    // long_row (32768 x 65536 x 256 with 132 per row 356 against 442 us,
+    // 2048 x 65536 x 256 with 500 per row 126 against 132), and rows of 512
+    // or more are split into segments (1024 x 65536 x 512 with 1000 per row:
+    // float4 13% faster).
+    const bool mid_rows = (nnz >= 64LL * M && nnz < 512LL * M) || (hint > kLongRow && hint < 2 * kSegLen);
+    const bool long_rows = hint > kLongRow || (hint < 0 && nnz > (long long)kLongRow * M);
+    const bool wide_band = (long long)K * kSliceWidth * 4 > kSliceCapBand;
+    if (mid_rows && !(wide_band && long_rows)) return CSRSPMM_ALGO_WARP_PER_ROW_SMEM;
   }
   if (algo == CSRSPMM_ALGO_AUTO && N % 4 == 0 && N < 128 && (long long)nnz >= 24LL * M &&
       per_call_panels(4, wants_plan(CSRSPMM_ALGO_WARP_PER_ROW_FP4, M, K, N, nnz, hint), K, N, nnz, hint) > 0) {

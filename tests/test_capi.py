@@ -78,7 +78,14 @@ def test_parse_and_names():
     # from N = 128, swept column slices take the float4 LDS-staged variant
     assert ex(6, 65536, 65536, 256, 4325376) == 5           # large
     assert ex(6, 65536, 65536, 256, 65536 * 7) == 3         # under 2 per band: merge blocks
-    assert ex(6, 32768, 65536, 256, 4325376) == 3           # too few rows to sweep
+    assert ex(6, 32768, 65536, 256, 4325376) == 3           # too few rows to sweep: a 16 MiB
+                                                            # band and rows above 128
+    assert ex(6, 32768, 65536, 256, 32768 * 40) == 3         # too few rows to sweep, 40 per row
+    # unswept slices of rows averaging 64..511: the scalar LDS form
+    assert ex(6, 4096, 65536, 128, 4096 * 128) == 4
+    assert ex(6, 32768, 32768, 256, 32768 * 300) == 4        # rows above 128 on an 8 MiB band
+    assert ex(6, 4096, 65536, 128, 4096 * 512) == 3          # 512 per row: split rows
+    assert ex(6, 4096, 65536, 128, 4096 * 63) == 3
     assert ex(6, 1 << 20, 1 << 20, 512, 16 << 20) == 3      # R-MAT N = 512: 0.25 per band
     # sliced calls of skewed rows (a hint above 128 and 4x the mean) take the scalar LDS form
     assert ex(6, 1 << 20, 1 << 20, 512, 16084813, 39531) == 4   # R-MAT N = 512 with its hint
@@ -89,9 +96,9 @@ def test_parse_and_names():
     # sliced calls that do not sweep, of rows of 129..511 nonzeros, take it too
     assert ex(6, 4096, 4096, 2048, 4096 * 300, 300) == 4
     assert ex(6, 8192, 16384, 512, 8192 * 300, 300) == 4
-    assert ex(6, 8192, 16384, 512, 8192 * 300, 128) == 3       # no long row
-    assert ex(6, 8192, 16384, 512, 8192 * 300, 512) == 3       # rows split into segments
-    assert ex(6, 8192, 16384, 512, 8192 * 300, -1) == 3        # no hint
+    assert ex(6, 8192, 16384, 512, 8192 * 40, 128) == 3        # short rows
+    assert ex(6, 8192, 16384, 512, 8192 * 600, 700) == 3       # rows split into segments
+    assert ex(6, 8192, 16384, 512, 8192 * 300, -1) == 4        # the mean tells without a hint
     assert ex(3, 4096, 4096, 128, 4096 * 200) == 3          # concrete ids pass through
     assert ex(9, 4096, 4096, 128, 4096 * 200) == -1
     assert lib.csrspmm_version() >= 100
