@@ -295,8 +295,8 @@ int resolve_algorithm(int algo, int M, int K, int N, int nnz, int hint) {
   }
   if (algo == CSRSPMM_ALGO_AUTO && N % 4 == 0 && N == 128 &&
       (M >= 4096 || (M >= 1024 && plan_skips(M, K, N, nnz, hint))) &&
-      (long long)K * N * 4 <= (4LL << 20) && (long long)nnz >= 160LL * M) {
-    // A B that stays in the L2s and rows of 160 nonzeros or more on average:
+      (long long)K * N * 4 <= (4LL << 20) && (long long)nnz >= 96LL * M) {
+    // A B that stays in the L2s and rows of 96 nonzeros or more on average:
     // the rows are long-row segments, and the scalar LDS-staged form keeps
     // more gathers in flight per row.  Measured on MI355X per call, uniform
     // rows at N = 128 with max_row_nnz given: M = 4096, K = 4096, 205 per row
@@ -306,7 +306,11 @@ int resolve_algorithm(int algo, int M, int K, int N, int nnz, int hint) {
     // the call as one launch (plan_skips), rows summed whole by one group
     // each: M = 1024, K = 2048, 200 per row 13.0 -> 10.5 us; M = 1536, K =
     // 8192, 220 per row 23.1 -> 16.4; M = 2048, K = 2048, 200 per row 13.6 ->
-    // 11.2; M = 1024, K = 1024, 160 per row 10.9 -> 10.0.
+    // 11.2; M = 1024, K = 1024, 160 per row 10.9 -> 10.0.  Rows of 96-159
+    // without a hint, M = 4096, K = 4096: 112 per row 23.9 -> 18.2 us, 128
+    // per row 29.9 -> 22.1, 144 per row 22.0 -> 21.5; M = 16384, K = 8192,
+    // 128 per row 77.0 -> 55.1; M = 8192, K = 8192, 120 per row 43.6 -> 36.5;
+    // 64 per row stays even (15.8 against 16.0 us).
     return CSRSPMM_ALGO_WARP_PER_ROW_SMEM;
   }
   return resolve_algorithm(algo, N);

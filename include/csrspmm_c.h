@@ -87,7 +87,7 @@ int csrspmm_resolve_algorithm(int algo, int N);
  *    with per-call column panels possible for float4 columns (a B of at
  *    least 64 MiB, a row of 1024 or more not ruled out) take the float4
  *    broadcast variant, which has the panels;
- *  - at N = 128 a B of at most 4 MiB with rows of 160 or more nonzeros on
+ *  - at N = 128 a B of at most 4 MiB with rows of 96 or more nonzeros on
  *    average (M >= 4096, or M >= 1024 when the hint lets the call run as
  *    one launch) takes the scalar LDS-staged variant;
  *  - from N = 128, a call cut into column slices whose hint exceeds both

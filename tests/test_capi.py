@@ -51,13 +51,14 @@ def test_parse_and_names():
     assert lib.csrspmm_resolve_algorithm(2, 128) == 2
     assert lib.csrspmm_resolve_algorithm(9, 128) == -1
     # From the whole shape: at N = 128 an L2-sized B (<= 4 MiB) with long rows
-    # (>= 160 per row on average, M >= 4096) takes WarpPerRowSmem
+    # (>= 96 per row on average, M >= 4096) takes WarpPerRowSmem
     def ex(a, M, K, N, nnz, hint=-1):
         return lib.csrspmm_resolve_algorithm_ex(a, M, K, N, nnz, hint)
     assert ex(6, 4096, 4096, 128, 4096 * 160) == 4
     assert ex(6, 4096, 8192, 128, 4096 * 160) == 4          # B exactly 4 MiB
     assert ex(6, 4096, 8193, 128, 4096 * 160) == 3          # B above 4 MiB
-    assert ex(6, 4096, 4096, 128, 4096 * 160 - 1) == 3      # rows shorter
+    assert ex(6, 4096, 4096, 128, 4096 * 96) == 4           # from 96 per row
+    assert ex(6, 4096, 4096, 128, 4096 * 96 - 1) == 3      # rows shorter
     assert ex(6, 4095, 4096, 128, 4095 * 200) == 3          # fewer rows
     assert ex(6, 1024, 2048, 128, 1024 * 200, 250) == 4     # one launch under the hint: from 1024 rows
     assert ex(6, 1023, 2048, 128, 1023 * 200, 250) == 3
