@@ -1131,7 +1131,14 @@ static hipError_t dispatch_vec4_cols(const Problem& p, hipStream_t s) {
   }
   const int t = (nv + 63) / 64;
   if (t <= 1) return launch_rg<4, 64, 1, kVec4U, LDS, SU, BUF>(p, s);
-  if (t <= 2) return launch_rg<4, 64, 2, 4, LDS, SU, BUF>(p, s);
+  // Beyond 512 columns a planned call loops over 512-column panels; one
+  // with rows summed whole (no plan) takes 1024 columns a pass, since each
+  // pass walks a row's chain again.  Measured on MI355X per call,
+  // bit-identical, 512 against 1024 columns a pass: 4096^2 x 1024 with 300
+  // per row 392 -> 287 us, 128 per row 154 -> 138, 8192 x 2048 x 2048 with
+  // 64 per row 269 -> 232 (213 -> 188 with the hint); rows summed whole,
+  // 2048 x 4096 x 1024 with 200 per row 61.0 against 64.1 us.
+  if (t <= 2 || p.plan) return launch_rg<4, 64, 2, 4, LDS, SU, BUF>(p, s);
   return launch_rg<4, 64, 4, 2, LDS, SU, BUF>(p, s);  // N > 1024 loops over 1024-column panels
 }
 
