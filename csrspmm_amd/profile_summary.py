@@ -231,6 +231,9 @@ def main(argv=None):
         key, entry = summarize(prof, name)
         entry["commit"] = commit
         traffic[key] = entry
+    # An entry whose summary file is gone describes a run nobody can read.
+    traffic = {k: v for k, v in traffic.items()
+               if os.path.exists(os.path.join(ROOT, "profiles", v.get("summary", "")))}
     with open(tj, "w") as f:
         json.dump(traffic, f, indent=1)
         f.write("\n")
