@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <map>
 #include <mutex>
 #include <thread>
@@ -23,8 +24,9 @@ WorkspaceLayout workspace_layout(int M, int K, int N, int nnz, int P) {
   WorkspaceLayout L{};
   const SegGeom g = seg_geom(nnz);
   L.nslots = nnz >> g.slot_shift;
-  // capacity for the merge blocks of either column width
-  L.nblocks = merge_blocks(M, nnz, std::min(merge_block(1, M, nnz), merge_block(4, M, nnz)));
+  // capacity for the merge blocks of either column width, sliced or not
+  L.nblocks = merge_blocks(
+      M, nnz, std::min({merge_block(1, M, nnz), merge_block(4, M, nnz), sliced_merge_block(M, nnz)}));
   L.ldp = ((long long)N + 3) & ~3LL;
   size_t off = 0;
   L.block_start_off = off;
@@ -465,7 +467,7 @@ int spmm_impl(int algo_in, int M, int K, int N, int nnz, const int* rowptr, cons
       // a workspace sized without the panel tables runs without panels
       if (ws_bytes < L.total) L = workspace_layout(M, K, N, nnz, 0);
     }
-    bind_workspace(p, ws, L, merge_block(vec, M, nnz));
+    bind_workspace(p, ws, L, call_merge_block(vec, M, nnz, p.sw > 0));
     set_row_hint(p, hint);
   }
   return to_status(launch_algorithm(algo, p, s));

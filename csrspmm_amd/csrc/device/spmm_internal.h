@@ -128,6 +128,34 @@ inline int merge_block(int vec, int M, int nnz) {
 inline int merge_blocks(int M, int nnz, int mblk) {
   return (int)(((long long)M + nnz + 1 + mblk - 1) / mblk);
 }
+// A per-call float4 call with column slices and fewer than
+// kSlicedMergeRowsMax rows sizes its merge blocks to the rows instead: the
+// largest power of two from 16 to 64 not above the mean row's items (1 + its
+// nonzeros).  Such a slice launch holds a round or two of 16-lane groups,
+// each on one block of whole rows, so the last round's few blocks set its
+// length; smaller blocks spread that tail over more, shorter rounds, and
+// rows longer than the block leave its groups idle.  Measured on MI355X per
+// call (N = 256, uniform rows, bit-identical), 64 -> this rule: 32768^2 with
+// 8 per row 50.8 -> 39.7 us, 16: 71.9 -> 58.4, 24: 97.9 -> 84.4, 40: 118.1
+// -> 113.8, 48: 187.3 -> 150.1; 16384 x 32768 with 16 per row 47.4 -> 35.9,
+// 32: 75.2 -> 56.0, 40: 87.7 -> 66.3; 8192 x 65536 x 1024 with 50 per row
+// 395 -> 257.  From 65536 rows the launches hold enough blocks that their
+// size hardly matters (65536 x 32768 and 131072^2 within 1%), and R-MAT's
+// 2^20 rows lost 7-14% with the small blocks.  Stored plans keep
+// merge_block (their tables serve every N).
+constexpr int kSlicedMergeBlockMin = 16;
+constexpr int kSlicedMergeRowsMax = 65536;
+inline int sliced_merge_block(int M, int nnz) {
+  if (M >= kSlicedMergeRowsMax) return merge_block(4, M, nnz);
+  const long long items = M > 0 ? ((long long)M + nnz) / M : 1;
+  int m = kSlicedMergeBlockMin;
+  while (m * 2 <= kMergeBlockVec4 && m * 2 <= items) m *= 2;
+  while (m > 1 && ((long long)M + nnz + 1) / m < kMinMergeBlocks) m >>= 1;
+  return m;
+}
+inline int call_merge_block(int vec, int M, int nnz, bool sliced) {
+  return vec == 4 && sliced ? sliced_merge_block(M, nnz) : merge_block(vec, M, nnz);
+}
 
 // Below this many (rows + nonzeros) the plan is skipped and each row is
 // processed whole by one group (one launch instead of three).

@@ -94,3 +94,33 @@ def test_slices_stored_plan(gpu):
         torch.cuda.synchronize()
         check(algo, dC.cpu().numpy(), rowptr, colidx, vals, B, what="stored plan, sliced")
         plan.close()
+
+
+@pytest.mark.parametrize("per_row", [3, 9, 20, 40, 70])
+@pytest.mark.parametrize("algo", ["WarpPerRowFp4", "WarpPerRowSmemFp4"])
+def test_sliced_merge_blocks_sized_to_rows(algo, per_row, gpu):
+    """A per-call float4 call with slices and fewer than 65536 rows sizes its
+    merge blocks from the mean row (16, 16, 16, 32 and 64 items here); a
+    stored plan keeps 64 (16 for the sparsest, by the block count floor).  Rows are summed whole either way, so the two agree bit for bit
+    (and with the fp32 restatement), including the empty rows spread among
+    them and rows longer than the block."""
+    K, N, M = 40000, 256, 20000  # B of 39 MiB: four 64-column slices
+    rng = np.random.default_rng(per_row)
+    lens = np.minimum(rng.integers(0, 2 * per_row + 1, M), 128).astype(np.int64)  # no long rows
+    lens[rng.choice(M, M // 10, replace=False)] = 0
+    rowptr, colidx, vals = csr_from_lengths(lens, K, seed=per_row)
+    B = gen.dense(24, gen.TAG_B, K, N)
+    print(f"[slices] merge blocks {algo} per_row={per_row} nnz={colidx.size}", flush=True)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(gpu)  # noqa: E731
+    drp, dci, dv, dB = t(rowptr), t(colidx), t(vals), t(B)
+    dC = torch.full((M, N), float("nan"), device=gpu)
+    capi.spmm(algo, drp, dci, dv, dB, dC, 1.0, 0.0)
+    plan = capi.Plan(algo, drp, dci, dv, K, n_hint=N)
+    dP = torch.full((M, N), float("nan"), device=gpu)
+    plan.spmm(dB, dP, 1.0, 0.0)
+    torch.cuda.synchronize()
+    plan.close()
+    C = dC.cpu().numpy()
+    check(algo, C, rowptr, colidx, vals, B, what=f"merge blocks, {per_row} per row")
+    assert np.array_equal(C.view(np.uint32), dP.cpu().numpy().view(np.uint32)), \
+        f"{algo}: per-call and stored-plan results differ"
