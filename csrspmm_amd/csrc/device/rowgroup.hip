@@ -1154,15 +1154,18 @@ static bool buf_gathers_ok(const Problem& p) {
 // The kernel shape comes from the columns one block covers: a column slice,
 // or all N.
 //
-// Unsliced float4 calls gather B through a buffer resource when it fits
+// Float4 calls gather B through a buffer resource when it fits
 // (buf_gathers_ok).  Measured on MI355X against 64-bit global loads, with
 // bit-identical results: XL 393.6 -> 376.3 us per call (VALU instructions
 // 133 M -> 59 M, L2 hit rate 0.50 -> 0.56, fetched bytes -12%), the
-// mean-98 power-law config 1085 -> 1071 us, medium 48.5 -> 45.1 us.  Sliced
-// calls keep global loads: the 65536 x 256 uniform config went 381 -> 423 us
-// with the same L2 requests and its hit rate falling 0.48 -> 0.39 (leaner
-// waves keep more rows of its 16 MiB band in flight), and 399 us at 4 or 5
-// blocks per CU; R-MAT N = 512 was unchanged.
+// mean-98 power-law config 1085 -> 1071 us, medium 48.5 -> 45.1 us.  On
+// column slices (those the band sweep does not take): power-law rows (mean
+// 32) at 32768^2 x 256 290 -> 199 us, uniform rows 4096 x 65536 x 256 with
+// 32 per row 41.7 -> 35.8, 8192 x 65536 x 1024 with 50 per row 257 -> 238,
+// 32768^2 x 256 with 24 per row 84.1 -> 80.1; R-MAT N = 256 and 512 -1% and
+// -0.3%; 131072^2 and power-law rows at K = 65536-131072 within 0.3%.  (The
+// uniform 65536 x 256 config, sliced without the sweep, had gone 381 -> 423
+// us with it, its L2 hit rate falling 0.48 -> 0.39; it sweeps now.)
 template <bool LDS>
 static hipError_t dispatch_vec4(const Problem& p, hipStream_t s) {
   // A column slice (64 columns: 16-lane groups) keeps 8 gathers in flight per
@@ -1179,6 +1182,7 @@ static hipError_t dispatch_vec4(const Problem& p, hipStream_t s) {
       sweep_geometry(p.K, p.sw, q.sweep_shift, q.sweep_bands);
       return launch_rg<4, 16, 1, kVec4U, LDS, CSRSPMM_SWEEP_SU, true, true>(q, s);
     }
+    if (buf_gathers_ok(p)) return launch_rg<4, 16, 1, kVec4U, LDS, 8, true>(p, s);
     return launch_rg<4, 16, 1, kVec4U, LDS, 8>(p, s);
   }
   if (buf_gathers_ok(p)) return dispatch_vec4_cols<LDS, true>(p, s);
