@@ -272,18 +272,20 @@ int resolve_algorithm(int algo, int M, int K, int N, int nnz, int hint) {
     // faster, of 64 at N = 256 1.3x; at M = K = 32768, N = 256 rows of 128
     // 357 -> 289 us and of 300 798 -> 632; 4096^2 x 2048 with 300 per row
     // 1368 -> 607 us, 2048 x 16384 x 1024 with 400 per row 388 -> 275.  On
-    // a 64-column band above kSliceCapBand (8 MiB), from 8192 rows, the
+    // a 64-column band above kSliceCapBand (8 MiB), from 4096 rows, the
     // float4 segments, 8 gathers deep under the residency cap, lead as soon
     // as rows exceed long_row (with the hint: 8192 x 65536 x 256 with 300 per
     // row 241 against 314 us, 16384 x 65536 x 256 with 200 per row 278
     // against 342, 32768 x 65536 x 256 with 132 per row 356 against 442;
-    // with 4096 rows the scalar form still leads, 195 against 163 us).  Rows
+    // 4096 x 65536 with 300 per row, since the float4 slices gather through
+    // a buffer resource: N = 128 73.2 against 86.3 us, 256 140.9 against
+    // 165.7, 1024 563 against 667).  Rows
     // of 512 or more are split into segments (1024 x 65536 x 512 with 1000
     // per row: float4 13% faster).
     const bool mid_rows = (nnz >= 64LL * M && nnz < 512LL * M) || (hint > kLongRow && hint < 2 * kSegLen);
     const bool long_rows = hint > kLongRow || (hint < 0 && nnz > (long long)kLongRow * M);
     const bool wide_band = (long long)K * kSliceWidth * 4 > kSliceCapBand;
-    if (mid_rows && !(wide_band && long_rows && M > 4096)) return CSRSPMM_ALGO_WARP_PER_ROW_SMEM;
+    if (mid_rows && !(wide_band && long_rows && M >= 4096)) return CSRSPMM_ALGO_WARP_PER_ROW_SMEM;
   }
   if (algo == CSRSPMM_ALGO_AUTO && N % 4 == 0 && N < 128 && (long long)nnz >= 24LL * M &&
       per_call_panels(4, wants_plan(CSRSPMM_ALGO_WARP_PER_ROW_FP4, M, K, N, nnz, hint), K, N, nnz, hint) > 0) {

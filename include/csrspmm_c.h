@@ -98,7 +98,7 @@ int csrspmm_resolve_algorithm(int algo, int N);
  *    takes the float4 LDS-staged variant;
  *  - and a sliced call that is not swept, of rows averaging 64 to 511
  *    nonzeros or with a hint of 129 to 511, takes the scalar LDS-staged
- *    variant, unless its 64-column band exceeds 8 MiB, M exceeds 4096 and
+ *    variant, unless its 64-column band exceeds 8 MiB, M is at least 4096 and
  *    rows exceed 128 (the hint, or the mean without one).
  * The SpMM entry points resolve Auto this way, and stored plans with the
  * true longest row.  No counterpart in the reference, whose Auto stub is

@@ -85,8 +85,9 @@ def test_parse_and_names():
     # unswept slices of rows averaging 64..511: the scalar LDS form
     assert ex(6, 4096, 65536, 128, 4096 * 128) == 4
     assert ex(6, 32768, 32768, 256, 32768 * 300) == 4        # rows above 128 on an 8 MiB band
-    assert ex(6, 4096, 65536, 256, 4096 * 300, 300) == 4     # a 16 MiB band, but few rows
-    assert ex(6, 8192, 65536, 256, 8192 * 300, 300) == 3     # a 16 MiB band from 8192 rows
+    assert ex(6, 4096, 65536, 256, 4096 * 300, 300) == 3     # a 16 MiB band from 4096 rows
+    assert ex(6, 2048, 65536, 256, 2048 * 300, 300) == 4     # but not fewer
+    assert ex(6, 8192, 65536, 256, 8192 * 300, 300) == 3
     assert ex(6, 4096, 65536, 128, 4096 * 512) == 3          # 512 per row: split rows
     assert ex(6, 4096, 65536, 128, 4096 * 63) == 3
     assert ex(6, 1 << 20, 1 << 20, 512, 16 << 20) == 3      # R-MAT N = 512: 0.25 per band
