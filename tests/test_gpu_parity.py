@@ -355,3 +355,31 @@ def test_reference_harness_known_answer(gpu):
     for algo in ALGORITHMS:
         C = run_spmm(algo, rowptr, colidx, vals, B, gpu, C0=C0, alpha=1.0, beta=0.5, hint=mx)
         assert np.all(C == np.float32(25597.5)), algo
+
+
+@pytest.mark.parametrize("per_row", [12, 40])
+@pytest.mark.parametrize("algo", ["WarpPerRowFp4", "WarpPerRowSmemFp4"])
+def test_unsliced_row_sized_merge_blocks(algo, per_row, gpu):
+    """An unsliced per-call float4 call of fewer than 65536 rows takes merge
+    blocks sized to its mean row (16 or 32 items here) when at least 16384
+    of them remain; a stored plan keeps 64.  Rows are summed whole either
+    way: the two agree bit for bit, and with the oracle."""
+    K, N, M = 20000, 128, 40000  # B of 10 MiB: no slices, no panels
+    rng = np.random.default_rng(200 + per_row)
+    lens = np.minimum(rng.integers(0, 2 * per_row + 1, M), 128).astype(np.int64)
+    rowptr, colidx, vals = csr_from_lengths(lens, K, seed=per_row)
+    B = gen.dense(25, gen.TAG_B, K, N)
+    print(f"[parity] row-sized merge blocks {algo} per_row={per_row} nnz={colidx.size}", flush=True)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(gpu)  # noqa: E731
+    drp, dci, dv, dB = t(rowptr), t(colidx), t(vals), t(B)
+    dC = torch.full((M, N), float("nan"), device=gpu)
+    capi.spmm(algo, drp, dci, dv, dB, dC, 1.0, 0.0)
+    plan = capi.Plan(algo, drp, dci, dv, K, n_hint=N)
+    dP = torch.full((M, N), float("nan"), device=gpu)
+    plan.spmm(dB, dP, 1.0, 0.0)
+    torch.cuda.synchronize()
+    plan.close()
+    C = dC.cpu().numpy()
+    assert_parity(algo, C, rowptr, colidx, vals, B, None, 1.0, 0.0, what=f"row-sized blocks {per_row}")
+    assert np.array_equal(C.view(np.uint32), dP.cpu().numpy().view(np.uint32)), \
+        f"{algo}: per-call and stored-plan results differ"
