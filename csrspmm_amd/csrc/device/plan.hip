@@ -163,9 +163,6 @@ int build_rowgroup_plan(csrspmm_plan_s* p, const std::vector<int>& rp, int n_hin
   if (!p->use_plan) return 0;
   const SegGeom g = seg_geom(nnz);
   p->nslots = maxlen <= g.long_row ? 0 : nnz >> g.slot_shift;  // no long row: no segment table
-  p->mblk = merge_block(vec, M, nnz);
-  p->nblocks = merge_blocks(M, nnz, p->mblk);
-
   // Panelized rows: long, on a large B, with non-decreasing columns; for
   // scalar columns from N = kPanelMinScalarN (measured on XL through a stored
   // plan: WarpPerRowSmem 625 -> 412 us, WarpPerRow 636 -> 513).
@@ -189,6 +186,13 @@ int build_rowgroup_plan(csrspmm_plan_s* p, const std::vector<int>& rp, int n_hin
   }
   std::vector<char> panelized((size_t)M, 0);
   for (int r : pan_rows) panelized[r] = 1;
+
+  // Merge blocks as a per-call call of the hinted width takes them (sized to
+  // the rows below 65536 of them); calls of another width run on them too.
+  const int nh = n_hint > 0 ? n_hint : 128;
+  const bool sliced = pan_rows.empty() && slice_width(K, nh, false, wide_sweep(vec, true, M, K, nnz)) > 0;
+  p->mblk = call_merge_block(vec, M, nnz, sliced);
+  p->nblocks = merge_blocks(M, nnz, p->mblk);
 
   // Merge-block starts and segment slots: the formulas of plan_kernel, with
   // panelized rows leaving their slots unused.

@@ -141,8 +141,8 @@ inline int merge_blocks(int M, int nnz, int mblk) {
 // 32: 75.2 -> 56.0, 40: 87.7 -> 66.3; 8192 x 65536 x 1024 with 50 per row
 // 395 -> 257.  From 65536 rows the launches hold enough blocks that their
 // size hardly matters (65536 x 32768 and 131072^2 within 1%), and R-MAT's
-// 2^20 rows lost 7-14% with the small blocks.  Stored plans keep
-// merge_block (their tables serve every N).
+// 2^20 rows lost 7-14% with the small blocks.  A stored plan takes the
+// blocks of its hinted width.
 constexpr int kSlicedMergeBlockMin = 16;
 constexpr int kSlicedMergeRowsMax = 65536;
 inline int sliced_merge_block(int M, int nnz) {

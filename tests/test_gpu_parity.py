@@ -362,8 +362,8 @@ def test_reference_harness_known_answer(gpu):
 def test_unsliced_row_sized_merge_blocks(algo, per_row, gpu):
     """An unsliced per-call float4 call of fewer than 65536 rows takes merge
     blocks sized to its mean row (16 or 32 items here) when at least 16384
-    of them remain; a stored plan keeps 64.  Rows are summed whole either
-    way: the two agree bit for bit, and with the oracle."""
+    of them remain, and so does a stored plan for that width.  Rows are
+    summed whole: the two agree bit for bit, and with the oracle."""
     K, N, M = 20000, 128, 40000  # B of 10 MiB: no slices, no panels
     rng = np.random.default_rng(200 + per_row)
     lens = np.minimum(rng.integers(0, 2 * per_row + 1, M), 128).astype(np.int64)

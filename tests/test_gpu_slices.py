@@ -100,10 +100,10 @@ def test_slices_stored_plan(gpu):
 @pytest.mark.parametrize("algo", ["WarpPerRowFp4", "WarpPerRowSmemFp4"])
 def test_sliced_merge_blocks_sized_to_rows(algo, per_row, gpu):
     """A per-call float4 call with slices and fewer than 65536 rows sizes its
-    merge blocks from the mean row (16, 16, 16, 32 and 64 items here); a
-    stored plan keeps 64 (16 for the sparsest, by the block count floor).  Rows are summed whole either way, so the two agree bit for bit
-    (and with the fp32 restatement), including the empty rows spread among
-    them and rows longer than the block."""
+    merge blocks from the mean row (16, 16, 16, 32 and 64 items here), and a
+    stored plan for that width does the same.  Rows are summed whole, so the
+    two agree bit for bit (and with the fp32 restatement), including the
+    empty rows spread among them and rows longer than the block."""
     K, N, M = 40000, 256, 20000  # B of 39 MiB: four 64-column slices
     rng = np.random.default_rng(per_row)
     lens = np.minimum(rng.integers(0, 2 * per_row + 1, M), 128).astype(np.int64)  # no long rows
