@@ -33,6 +33,7 @@ HIP_API = {
     "csrspmm_workspace_bytes_ex": (_c_size_t, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
     "csrspmm_workspace_panel_info": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
                                               ctypes.POINTER(_c_ll)]),
+    "csrspmm_call_shares": (_c_int, [_c_int] * 6),
     "csrspmm_spmm_f32": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p, _c_void_p,
                                   _c_void_p, _c_int, _c_void_p, _c_ll, _c_void_p, _c_ll, _c_float,
                                   _c_float, _c_void_p]),
@@ -196,6 +197,15 @@ def spmm(algo, rowptr, colidx, vals, B, C, alpha, beta, *, M=None, K=None, hint=
                                      _ptr(workspace), wsz, ctypes.c_void_p(stream))
     check(st, f"csrspmm_spmm {algo}")
     return C
+
+
+def call_shares(algo, M, K, N, nnz, hint=-1) -> bool:
+    """Whether a per-call product of this shape (workspace of
+    csrspmm_workspace_bytes_ex bytes, 16-byte aligned B and C rows) splits
+    its long rows by XCD, so that rows above 128 nonzeros are summed in
+    parts rather than in CSR order."""
+    a = ALGO[algo] if isinstance(algo, str) else int(algo)
+    return bool(hip().csrspmm_call_shares(a, M, K, N, nnz, hint))
 
 
 def panelized_rows(algo, rowptr, colidx, vals, B, C, alpha=1.0, beta=0.0, *, hint=-1):

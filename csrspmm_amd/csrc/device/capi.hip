@@ -20,7 +20,7 @@ namespace csrspmm_hip {
 
 static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-WorkspaceLayout workspace_layout(int M, int K, int N, int nnz, int P) {
+WorkspaceLayout workspace_layout(int M, int K, int N, int nnz, int P, bool shares) {
   WorkspaceLayout L{};
   const SegGeom g = seg_geom(nnz);
   L.nslots = nnz >> g.slot_shift;
@@ -62,6 +62,14 @@ WorkspaceLayout workspace_layout(int M, int K, int N, int nnz, int P) {
     off = align256(off + (size_t)(kPanelHist + P) * sizeof(int));
     L.part_off = off;
     off = align256(off + (size_t)L.nl_max * (size_t)P * (size_t)L.ldp * sizeof(float));
+  } else if (shares) {
+    L.shares = true;
+    L.shr_cb_off = off;
+    off = align256(off + (size_t)kXcds * sizeof(int));
+    L.shr_pb_off = off;
+    off = align256(off + (size_t)L.nslots * 2 * sizeof(int4));  // 8 ints per slot
+    L.shr_part_off = off;
+    off = align256(off + ((size_t)(nnz >> kShareIdxShift) + 1) * (size_t)L.ldp * sizeof(float));
   }
   L.total = off;
   return L;
@@ -92,6 +100,10 @@ void bind_workspace(Problem& p, void* ws, const WorkspaceLayout& L, int mblk) {
     p.dp.part = reinterpret_cast<float*>(b + L.part_off);
     p.dp_flag = reinterpret_cast<unsigned char*>(b + L.flag_off);
   }
+  p.shares = L.shares;
+  p.shr_cb = L.shares ? reinterpret_cast<int*>(b + L.shr_cb_off) : nullptr;
+  p.shr_pb = L.shares ? reinterpret_cast<int4*>(b + L.shr_pb_off) : nullptr;
+  p.shr_part = L.shares ? reinterpret_cast<float*>(b + L.shr_part_off) : nullptr;
 }
 
 int per_call_panels(int vec, bool plan, int K, int N, int nnz, int hint) {
@@ -453,12 +465,12 @@ int spmm_impl(int algo_in, int M, int K, int N, int nnz, const int* rowptr, cons
     p.sw = slice_width(K, N, P > 0, wide_sweep(vec, true, M, K, nnz));
     p.slice_launch = slice_launches(M, nnz);
     if (p.sw > 0) P = 0;  // a sliced call gathers band by band instead
-    WorkspaceLayout L = workspace_layout(M, K, N, nnz, P);
+    WorkspaceLayout L = workspace_layout(M, K, N, nnz, P, share_applies(true, K, N, nnz, p.sw, P, hint));
     if (owned) {
       lock = std::unique_lock<std::mutex>(g_ws_mutex);
       st = owned_workspace_locked(stream, L.total, &ws);
       if (st == CSRSPMM_STATUS_ALLOC_FAILED && L.total > L.base_total) {
-        // no room for the panel tables: run without them
+        // no room for the panel or share tables: run without them
         L = workspace_layout(M, K, N, nnz, 0);
         st = owned_workspace_locked(stream, L.total, &ws);
       }
@@ -466,7 +478,7 @@ int spmm_impl(int algo_in, int M, int K, int N, int nnz, const int* rowptr, cons
     } else {
       if (!ws || ws_bytes < L.base_total) return CSRSPMM_STATUS_WORKSPACE_TOO_SMALL;
       if (reinterpret_cast<uintptr_t>(ws) & 255) return CSRSPMM_STATUS_INVALID_VALUE;
-      // a workspace sized without the panel tables runs without panels
+      // a workspace sized without the panel or share tables runs without them
       if (ws_bytes < L.total) L = workspace_layout(M, K, N, nnz, 0);
     }
     bind_workspace(p, ws, L, call_merge_block(vec, M, nnz, p.sw > 0));
@@ -619,20 +631,32 @@ size_t csrspmm_workspace_bytes(int algo, int M, int N, int nnz) {
 }
 
 // The panels of a per-call product as far as the shape tells (pointer
-// alignment is checked per call); -1 when the call makes no plan.
-static int shape_panels(int algo, int M, int K, int N, int nnz, int hint) {
+// alignment is checked per call), as spmm_impl decides them; -1 when the
+// call makes no plan.  *shares: the call splits its long rows by XCD.
+static int shape_panels(int algo, int M, int K, int N, int nnz, int hint, bool* shares = nullptr) {
+  if (shares) *shares = false;
   algo = resolve_algorithm(algo, M, K, N, nnz, hint);
   if (M <= 0 || N <= 0 || nnz < 0 || K < 0 || !wants_plan(algo, M, K, N, nnz, hint)) return -1;
   const bool fp4 = (algo == CSRSPMM_ALGO_WARP_PER_ROW_FP4 || algo == CSRSPMM_ALGO_WARP_PER_ROW_SMEM_FP4) &&
                    N % 4 == 0;
-  int P = per_call_panels(fp4 ? 4 : 1, true, K, N, nnz, hint);
-  if (slice_width(K, N, P > 0) > 0) P = 0;
+  const int vec = fp4 ? 4 : 1;
+  int P = per_call_panels(vec, true, K, N, nnz, hint);
+  const int sw = slice_width(K, N, P > 0, wide_sweep(vec, true, M, K, nnz));
+  if (sw > 0) P = 0;
+  if (shares) *shares = share_applies(true, K, N, nnz, sw, P, hint);
   return P;
 }
 
 size_t csrspmm_workspace_bytes_ex(int algo, int M, int K, int N, int nnz, int max_row_nnz_hint) {
-  const int P = shape_panels(algo, M, K, N, nnz, max_row_nnz_hint);
-  return P < 0 ? 0 : workspace_layout(M, K, N, nnz, P).total;
+  bool shares = false;
+  const int P = shape_panels(algo, M, K, N, nnz, max_row_nnz_hint, &shares);
+  return P < 0 ? 0 : workspace_layout(M, K, N, nnz, P, shares).total;
+}
+
+int csrspmm_call_shares(int algo, int M, int K, int N, int nnz, int max_row_nnz_hint) {
+  bool shares = false;
+  const int P = shape_panels(algo, M, K, N, nnz, max_row_nnz_hint, &shares);
+  return P >= 0 && shares ? 1 : 0;
 }
 
 int csrspmm_workspace_panel_info(int algo, int M, int K, int N, int nnz, int max_row_nnz_hint,

@@ -790,19 +790,110 @@ __device__ __forceinline__ void plan_row_entries(const Problem& p, int r, int b_
 #endif
 constexpr int kPlanSoloEntries = CSRSPMM_PLAN_SOLO_ENTRIES;
 
+// Column boundaries of the XCD shares (the first block of plan_kernel, 256
+// threads, next to the row blocks): the columns at kShareSamples hashed
+// positions of colidx, counted in kShareBins bins of 2^hs columns;
+// boundary x (x = 1 .. 7) is the first column of the first bin whose
+// inclusive count reaches x / kXcds of the sample, so each XCD range carries
+// about an eighth of it.  Boundary 0 is 0 and boundary kXcds is K.  Only the
+// locality depends on them.  (Computing them in every block of plan_kernel
+// from the same sample took 16.7 M L2 requests on R-MAT: plan_kernel 13 ->
+// 223 us; in block 0, which holds the first and often longest rows, 12 ->
+// 24 us.)
+__device__ __forceinline__ void share_cut(const Problem& p) {
+  __shared__ int hist[kShareBins];
+  constexpr int kPer = kShareSamples / 256;
+  constexpr int kBinsPerLane = kShareBins / 64;
+  const int t = (int)threadIdx.x;
+  for (int i = t; i < kShareBins; i += 256) hist[i] = 0;
+  int hs = 0;
+  while (((long long)(p.K - 1) >> hs) >= kShareBins) ++hs;
+  // positions from a multiplicative hash of the sample index: evenly spaced
+  // ones fall on the same place in every row when the spacing is a multiple
+  // of the row length (uniform rows of 200 over 52 M nonzeros: every sample
+  // a row's smallest column, and one XCD range held 99% of the nonzeros)
+  int cv[kPer];
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const unsigned long long i = (unsigned long long)(u * 256 + t) + 1;
+    const unsigned long long h = (i * 0x9E3779B97F4A7C15ull) >> 32;
+    cv[u] = p.nnz > 0 ? p.colidx[(int)(h % (unsigned long long)p.nnz)] : -1;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < kPer; ++u)
+    if (cv[u] >= 0 && cv[u] < p.K) atomicAdd(&hist[cv[u] >> hs], 1);
+  __syncthreads();
+  if (t >= 64) return;
+  int h[kBinsPerLane];
+  int mine = 0;
+#pragma unroll
+  for (int b = 0; b < kBinsPerLane; ++b) {
+    h[b] = hist[t * kBinsPerLane + b];
+    mine += h[b];
+  }
+  int incl = mine;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int o = __shfl_up(incl, off);
+    if (t >= off) incl += o;
+  }
+  const long long total = __shfl(incl, 63);
+  int run = incl - mine;
+  int below[kXcds - 1];
+#pragma unroll
+  for (int x = 0; x < kXcds - 1; ++x) below[x] = 0;
+#pragma unroll
+  for (int b = 0; b < kBinsPerLane; ++b) {
+    run += h[b];
+#pragma unroll
+    for (int x = 0; x < kXcds - 1; ++x) below[x] += (long long)run * kXcds < (long long)(x + 1) * total;
+  }
+#pragma unroll
+  for (int x = 0; x < kXcds - 1; ++x)
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) below[x] += __shfl_xor(below[x], off);
+  if (t == 0) {
+#pragma unroll
+    for (int x = 0; x < kXcds - 1; ++x) {
+      const long long c = total > 0 ? (long long)below[x] << hs : (long long)p.K * (x + 1) / kXcds;
+      p.shr_cb[x] = (int)min(c, (long long)p.K);
+    }
+  }
+}
+
+// The boundaries 1 .. kXcds - 1 plan_kernel wrote, made non-decreasing and
+// clamped to [0, K].
+__device__ __forceinline__ void share_cols(const Problem& p, int (&cb)[kXcds - 1]) {
+  int prev = 0;
+#pragma unroll
+  for (int x = 0; x < kXcds - 1; ++x) {
+    prev = min(max(p.shr_cb[x], prev), p.K);
+    cb[x] = prev;
+  }
+}
+
 // One thread per row r in [0, M]: the merge-block starts that fall on r, the
 // segment slots r owns and, with column panels, the windows that begin in r.
 // Every entry the main kernel reads is written here on each call, from
-// rowptr alone (no atomics); with panels, block 0 also zeroes the sampled
-// panel loads that panel_window_kernel adds to.
+// rowptr alone (no atomics); with panels, the first row block also zeroes
+// the sampled panel loads that panel_window_kernel adds to.  With XCD shares
+// the grid has one more block, the first, which only writes the shares'
+// column boundaries (share_cut) while the row blocks run.
 __global__ __launch_bounds__(256) void plan_kernel(Problem p) {
-  const int stride = gridDim.x * blockDim.x;
+  const int first = p.shares ? 1 : 0;  // blocks before the row blocks
+  if ((int)blockIdx.x < first) {
+    share_cut(p);
+    return;
+  }
+  const int rblock = (int)blockIdx.x - first;
+  const int stride = ((int)gridDim.x - first) * blockDim.x;
   const int mshift = __builtin_ctz((unsigned)p.mblk);  // mblk is a power of two
   const int lane = lane_id();
-  if (p.dp.P > 0 && blockIdx.x == 0)
+  if (p.dp.P > 0 && rblock == 0)
     for (int q = (int)threadIdx.x; q < p.dp.P; q += blockDim.x) p.dp.sched[kPanelHist + q] = 0;
   // block-uniform trip count, so every wave reaches the ballot below whole
-  for (int base = blockIdx.x * blockDim.x; base <= p.M; base += stride) {
+  for (int base = rblock * blockDim.x; base <= p.M; base += stride) {
     const int r = base + (int)threadIdx.x;
     int b_lo = 0, b_hi = -1, s0 = 0, s1 = 0, nseg = 0, w0 = 0, w1 = 0, x0 = 0, x1 = 0;
     if (r <= p.M) {
@@ -840,6 +931,252 @@ __global__ __launch_bounds__(256) void plan_kernel(Problem p) {
                        __builtin_amdgcn_readlane(w0, l), __builtin_amdgcn_readlane(w1, l),
                        __builtin_amdgcn_readlane(x0, l), __builtin_amdgcn_readlane(x1, l), lane, 64);
     }
+  }
+}
+
+// XCD shares (Problem::shares).  The first slot s of a split row (fewer
+// than kShareSplitSegs segments) keeps, at shr_pb + 8 s, the offsets
+// [0 .. 6] = o_1 .. o_7 from the row start at which the parts of column
+// ranges 1 .. 7 begin (o_0 = 0, o_8 = the row length; o_x counts the row's
+// nonzeros whose column lies below boundary x).  Slot s holding segment k of
+// a longer row keeps at [7] the range holding the column at the segment's
+// middle, the XCD that sums the whole segment.  For a sorted row part x
+// holds the columns of range x; for any row the parts partition its
+// positions, since the boundaries (made non-decreasing) make o_x
+// non-decreasing in x.
+
+// Segment k of a long row [rs, re): its positions [start, end).
+__device__ __forceinline__ void segment_range(const Problem& p, int rs, int re, int k, int& start,
+                                              int& end, int& nseg) {
+  const int len = re - rs;
+  nseg = seg_count(p, len);
+  start = rs + seg_begin(len, nseg, k);
+  end = rs + seg_begin(len, nseg, k + 1);
+}
+
+// Slots per wave of share_bounds_kernel, and slots whose columns load
+// together; build-time tunable.  Measured on MI355X (R-MAT N = 64), slots x
+// batch: 16 x 4 37.5 us, 32 x 2 40.0, 16 x 2 30.3, 8 x 2 27.3, 4 x 2 29.9,
+// 4 x 1 23.0, 2 x 1 26.7, 1 x 1 32.5: short waves, many of them.
+#ifndef CSRSPMM_SHARE_BOUND_SLOTS
+#define CSRSPMM_SHARE_BOUND_SLOTS 4
+#endif
+#ifndef CSRSPMM_SHARE_BOUND_BATCH
+#define CSRSPMM_SHARE_BOUND_BATCH 1
+#endif
+constexpr int kShareBoundSlots = CSRSPMM_SHARE_BOUND_SLOTS;
+
+// The share table (shr_pb) of every slot, after plan_kernel: one wave per
+// kShareBoundSlots slots, balanced by nonzeros rather than rows (R-MAT's
+// long rows crowd a few row blocks).  Lane t loads slot t's metadata (two
+// rounds for all of them); then the slots to record, four at a time, load
+// their columns in rounds of 512 positions each (a split row's, or a whole
+// segment's middle one), and count them against the boundaries by ballots.
+__global__ __launch_bounds__(256) void share_bounds_kernel(Problem p) {
+  constexpr int S = kShareBoundSlots;
+  constexpr int kB = CSRSPMM_SHARE_BOUND_BATCH;
+  constexpr int kC = 8;  // chunks of 64 positions per slot and round
+  static_assert(S <= 64, "one slot per lane");
+  const int lane = lane_id();
+  const int s0 = ((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6)) * S;
+  int cb[kXcds - 1];
+  share_cols(p, cb);
+  // lane t < S: slot s0 + t
+  int2 si = make_int2(-1, 0);
+  if (lane < S && s0 + lane < p.nslots) si = p.seg_info[s0 + lane];
+  if (si.x >= p.M) si.x = -1;
+  // split: -1 nothing to record, 0 a segment kept whole (its middle
+  // position in st), 1 the first slot of a split row (its positions
+  // [st, en) are the whole row)
+  int st = 0, en = 0, split = -1;
+  if (si.x >= 0) {
+    const int rs = clamp_nnz(p.rowptr[si.x], p.nnz);
+    const int re = max(clamp_nnz(p.rowptr[si.x + 1], p.nnz), rs);
+    int nseg, a, e;
+    segment_range(p, rs, re, si.y, a, e, nseg);
+    if (nseg < kShareSplitSegs) {
+      split = si.y == 0 && nseg > 0 ? 1 : -1;
+      st = rs;
+      en = re;
+    } else if (si.y < nseg) {
+      split = 0;
+      st = (a + e) >> 1;
+      en = st + 1;
+    }
+  }
+  unsigned long long todo = __ballot(split >= 0);
+  while (todo) {
+    int l[kB], a[kB], e[kB], sp[kB];
+#pragma unroll
+    for (int b = 0; b < kB; ++b) {
+      l[b] = todo ? __ffsll((long long)todo) - 1 : -1;
+      if (todo) todo &= todo - 1;
+      a[b] = l[b] >= 0 ? __builtin_amdgcn_readlane(st, l[b]) : 0;
+      e[b] = l[b] >= 0 ? __builtin_amdgcn_readlane(en, l[b]) : 0;
+      sp[b] = l[b] >= 0 ? __builtin_amdgcn_readlane(split, l[b]) : -1;
+    }
+    int cnt[kB][kXcds - 1];
+#pragma unroll
+    for (int b = 0; b < kB; ++b)
+#pragma unroll
+      for (int x = 0; x < kXcds - 1; ++x) cnt[b][x] = 0;
+    int mx = 0;  // the longest of the batch's ranges
+#pragma unroll
+    for (int b = 0; b < kB; ++b) mx = max(mx, e[b] - a[b]);
+    for (int off = 0; off < mx; off += kC * 64) {
+      int cv[kB][kC];
+#pragma unroll
+      for (int b = 0; b < kB; ++b)
+#pragma unroll
+        for (int u = 0; u < kC; ++u) {
+          const int j = a[b] + off + u * 64 + lane;
+          cv[b][u] = j < e[b] ? p.colidx[j] : 0x7fffffff;
+        }
+#pragma unroll
+      for (int b = 0; b < kB; ++b)
+#pragma unroll
+        for (int u = 0; u < kC; ++u)
+#pragma unroll
+          for (int x = 0; x < kXcds - 1; ++x) cnt[b][x] += __popcll(__ballot(cv[b][u] < cb[x]));
+    }
+#pragma unroll
+    for (int b = 0; b < kB; ++b) {
+      if (sp[b] < 0 || lane != 0) continue;
+      int* dst = reinterpret_cast<int*>(p.shr_pb) + 8LL * (s0 + l[b]);
+      if (sp[b] == 0) {
+        // a whole segment: the range of its middle column (one position)
+        int x = 0;
+#pragma unroll
+        for (int i = 0; i < kXcds - 1; ++i) x += 1 - cnt[b][i];
+        dst[7] = x;
+      } else {
+        int4* d4 = reinterpret_cast<int4*>(dst);
+        d4[0] = make_int4(cnt[b][0], cnt[b][1], cnt[b][2], cnt[b][3]);
+        d4[1] = make_int4(cnt[b][4], cnt[b][5], cnt[b][6], -1);
+      }
+    }
+  }
+}
+
+// B-row gathers in flight per lane in the scalar-column share_kernel's
+// pieces (at least the variant's own; float4 ones keep theirs), and the
+// slots one group of it takes (one per lane, at most G); build-time tunable.
+#ifndef CSRSPMM_SHARE_U
+#define CSRSPMM_SHARE_U 16
+#endif
+#ifndef CSRSPMM_SHARE_LANES
+#define CSRSPMM_SHARE_LANES 64
+#endif
+
+// The long rows of a call with XCD shares, over the columns of the slices
+// [slice0, slice0 + gridDim.x / share_blocks): block b runs on XCD
+// x = b mod kXcds.  Group g of XCD x's blocks (g = (b / kXcds) * GPB +
+// group, ng groups in all) takes G slots, lane l slot g + l * ng, so that a
+// long row's neighbouring segments (which fall in one column range) go to
+// different groups.  Each lane loads its slot's metadata (three rounds for
+// the group); then the group walks its slots with something to do in lane
+// order, the next one's first chunk of (col, val) loaded while the current
+// one is summed: at a split row's first slot, part x of the row (zero when
+// empty) into its shr_part row, or, for a segment kept whole whose middle
+// column lies in range x, the whole segment into its segment partial.  Launched before the
+// main kernel of the same slices, which then holds no segment blocks.
+template <int VEC, int G, int T, int US, bool LDS, bool BUF>
+__global__ __launch_bounds__(kWaves * 64) void share_kernel(Problem p, int share_blocks, int slice0) {
+  using VT = typename Vec<VEC>::T;
+  constexpr int GPW = 64 / G;
+  constexpr int GPB = kWaves * GPW;
+  constexpr int PW = G * VEC * T;
+  constexpr int UP = (VEC == 4 || US >= CSRSPMM_SHARE_U) ? US : (CSRSPMM_SHARE_U < G ? CSRSPMM_SHARE_U : G);
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int gl = lane & (G - 1);
+  const int gbase = lane & ~(G - 1);
+  const int gid = G == 64 ? wave : wave * GPW + lane / G;
+  const unsigned long long gmask = G == 64 ? ~0ULL : (((1ULL << G) - 1ULL) << gbase);
+  __shared__ int2 stage_all[LDS ? kWaves * 64 : 1];
+  int2* stage = stage_all + (LDS ? wave * 64 : 0);
+
+  int bid = (int)blockIdx.x;
+  int c_lo = 0, c_hi = p.N;
+  if (p.sw > 0) {
+    const int local = bid / share_blocks;
+    bid -= local * share_blocks;
+    c_lo = (slice0 + local) * p.sw;
+    c_hi = min(p.N, c_lo + p.sw);
+  }
+  constexpr int SL = CSRSPMM_SHARE_LANES < G ? CSRSPMM_SHARE_LANES : G;  // slots per group
+  const int x = (int)(blockIdx.x % kXcds);  // share_blocks is a multiple of kXcds
+  const int ng = share_blocks / kXcds * GPB;
+  const int s = gl < SL ? ((bid / kXcds) * GPB + gid) + gl * ng : 0x7fffffff;
+
+  // this lane's slot: the positions [pa, pe) and the partial row (-1:
+  // nothing to do; <= -2: segment partial -2 - prow)
+  int pa = 0, pe = 0;
+  long long prow = -1;
+  int2 si = s < p.nslots ? p.seg_info[s] : make_int2(-1, 0);  // (s past nslots beyond SL lanes)
+  if (si.x >= p.M) si.x = -1;
+  if (si.x >= 0) {
+    const int rs = clamp_nnz(p.rowptr[si.x], p.nnz);
+    const int re = max(clamp_nnz(p.rowptr[si.x + 1], p.nnz), rs);
+    int start, end, nseg;
+    segment_range(p, rs, re, si.y, start, end, nseg);
+    const int* pb = reinterpret_cast<const int*>(p.shr_pb) + 8LL * s;
+    if (nseg >= kShareSplitSegs) {
+      if (si.y < nseg && pb[7] == x) {
+        pa = start;
+        pe = end;
+        prow = -2 - ((long long)(rs >> p.seg_shift) + si.y);
+      }
+    } else if (si.y == 0 && nseg > 0) {
+      const int len = re - rs;
+      const int lo = x == 0 ? 0 : min(max(pb[x - 1], 0), len);
+      const int hi = x == kXcds - 1 ? len : min(max(pb[x], lo), len);
+      pa = rs + lo;
+      pe = rs + hi;
+      prow = (long long)(rs >> kShareIdxShift) + x;
+    }
+  }
+  unsigned long long todo = __ballot(prow != -1) & gmask;
+  // the first piece's first chunk
+  int l = todo ? __ffsll((long long)todo) - 1 - gbase : -1;
+  int a = l >= 0 ? group_bcast<G>(pa, gbase, l) : 0;
+  int e = l >= 0 ? group_bcast<G>(pe, gbase, l) : 0;
+  int cj;
+  float vj;
+  load_chunk(p, a, e, gl, cj, vj);
+  while (l >= 0) {
+    todo &= todo - 1;
+    const long long pr = ((long long)group_bcast<G>((int)(prow >> 32), gbase, l) << 32) |
+                         (unsigned)group_bcast<G>((int)prow, gbase, l);
+    // the next piece and its first chunk
+    const int ln = todo ? __ffsll((long long)todo) - 1 - gbase : -1;
+    const int an = ln >= 0 ? group_bcast<G>(pa, gbase, ln) : 0;
+    const int en = ln >= 0 ? group_bcast<G>(pe, gbase, ln) : 0;
+    int cn;
+    float vn;
+    load_chunk(p, an, en, gl, cn, vn);
+    float* dst = pr >= 0 ? p.shr_part + pr * p.ldp : p.partials + (-2 - pr) * p.ldp;
+    for (int c0 = c_lo; c0 < c_hi; c0 += PW) {
+      const Panel<VEC, G, T, BUF> pn(p, c0, gl, c_hi);
+      VT acc[T];
+#pragma unroll
+      for (int u = 0; u < T; ++u) acc[u] = Vec<VEC>::zero();
+      if (c0 != c_lo) load_chunk(p, a, e, gl, cj, vj);
+      stream_nonzeros_from<VEC, G, T, UP, LDS, BUF>(p, pn, a, e, cj, vj, gl, gbase, stage,
+                                                    [&](int, float v, const VT(&b)[T]) {
+#pragma unroll
+                                                      for (int u = 0; u < T; ++u) acc[u] = fma_v(v, b[u], acc[u]);
+                                                    });
+#pragma unroll
+      for (int u = 0; u < T; ++u) {
+        if (pn.cval[u]) *reinterpret_cast<VT*>(dst + pn.col[u]) = acc[u];
+      }
+    }
+    l = ln;
+    a = an;
+    e = en;
+    cj = cn;
+    vj = vn;
   }
 }
 
@@ -921,21 +1258,9 @@ __device__ __forceinline__ void store_cols4(const Problem& p, float* cptr, int c
 
 // Table slots one wave of the combine scan reads at once.  A split row (two
 // segments or more) owns two slots or more, so a wave meets at most
-// kScanSlots / 2 rows to sum.
+// kScanSlots / 2 rows to sum (with XCD shares, kScanSlots rows).
 constexpr int kScanSlots = 16;
 
-// C rows of split long rows (one partial per segment) and of panelized rows
-// (one partial per piece), each the sum of its partials in a fixed order, so
-// results repeat bit for bit.  A wave's lanes form P = 64 / GC groups of GC
-// lanes, each group covering 4 * GC columns (float4 per lane).
-//  * Blocks [0, scan_blocks): a wave reads kScanSlots consecutive table
-//    slots, loads the length of every row whose first segment lies among
-//    them (all at once), and sums the partials of each such row that has two
-//    segments or more: group q takes partials q, q + P, ..., then the P group
-//    sums meet in the xor tree.
-//  * Blocks [scan_blocks, ...): one panelized row per block.  Its 4 waves'
-//    4P groups split the pieces the same way; each wave's sum goes to LDS and
-//    wave 0 adds the four in wave order.
 template <int VEC, int GC>
 __global__ __launch_bounds__(kWaves * 64) void combine_kernel(Problem p, int scan_blocks) {
   constexpr int P = 64 / GC;
@@ -949,21 +1274,48 @@ __global__ __launch_bounds__(kWaves * 64) void combine_kernel(Problem p, int sca
       const int s = ch * kScanSlots + lane;
       int2 si = make_int2(-1, 1);
       if (lane < kScanSlots && s < p.nslots) si = p.seg_info[s];
-      int nseg = 0, x0 = 0;
+      int nseg = 0, x0 = 0, len = 0;
       if (si.x >= 0 && si.x < p.M && si.y == 0) {
         x0 = clamp_nnz(p.rowptr[si.x], p.nnz);
-        const int len = clamp_nnz(p.rowptr[si.x + 1], p.nnz) - x0;
+        len = max(clamp_nnz(p.rowptr[si.x + 1], p.nnz) - x0, 0);
         nseg = seg_count(p, len);
-        // one segment: stored by the segment phase; panelized: summed from pieces
-        if (nseg < 2 || (len >= kPanelMinLen && is_panelized(p, x0))) nseg = 0;
+        // one segment: stored by the segment phase; panelized: summed from
+        // pieces; split by XCD: summed from its parts whatever nseg
+        if (!p.shares && (nseg < 2 || (len >= kPanelMinLen && is_panelized(p, x0)))) nseg = 0;
       }
       unsigned long long rows = __ballot(nseg > 0);
+      if (p.shares) {
+        // Rows split by XCD, P at a time: lane group q takes the q-th and
+        // adds its kXcds part rows from x0 >> kShareIdxShift (zero where a
+        // part is empty) in range order, all loads in flight.
+        unsigned long long srows = __ballot(nseg > 0 && nseg < kShareSplitSegs);
+        rows &= ~srows;
+        while (srows) {
+          unsigned long long m = srows;
+          for (int i = 0; i < q; ++i) m &= m - 1;
+          const int lq = m ? __ffsll((long long)m) - 1 : -1;
+#pragma unroll
+          for (int i = 0; i < P; ++i) srows &= srows - 1;
+          const int src = lq >= 0 ? lq : 0;
+          const int row = __shfl(si.x, src);
+          const int rx0 = __shfl(x0, src);
+          if (lq < 0) continue;
+          const float* base = p.shr_part + (long long)(rx0 >> kShareIdxShift) * p.ldp;
+          float* crow = p.C + (long long)row * p.ldc;
+          for (int c0 = 0; c0 < p.N; c0 += GC * 4) {
+            const int c = c0 + gl * 4;
+            const bool cv = c < p.N;
+            const f4 acc = sum_strided<1>(base + c, nullptr, kXcds, 0, p.ldp, cv);
+            if (cv) store_cols4<VEC>(p, crow + c, c, acc);
+          }
+        }
+      }
       while (rows) {
         const int l = __ffsll((long long)rows) - 1;
         rows &= rows - 1;
         const int row = __builtin_amdgcn_readlane(si.x, l);
         const int n = __builtin_amdgcn_readlane(nseg, l);
-        // the row's partials x0 / kSegLen .. + n - 1
+        // the row's partials x0 / seg .. + n - 1
         const float* base = p.partials + (long long)(__builtin_amdgcn_readlane(x0, l) >> p.seg_shift) * p.ldp;
         float* crow = p.C + (long long)row * p.ldc;
         for (int c0 = 0; c0 < p.N; c0 += GC * 4) {
@@ -1042,8 +1394,15 @@ hipError_t launch_rg(const Problem& p, hipStream_t s) {
   constexpr int GPB = kWaves * (64 / G);
   const int units = SWEEP ? div_up_host(p.M, kSweepRows) : p.plan ? p.nblocks : p.M;
   const int unit_blocks = div_up_host(units, GPB);
+  // With XCD shares the segments run in share_kernel, launched before each
+  // main launch over the same slices, and the main launch has no segment
+  // blocks.
+  const bool shares = p.plan && p.nslots > 0 && p.shares;
   const int seg_blocks =
-      (p.plan && p.nslots > 0) ? std::min(kSegBlocksMax, div_up_host(p.nslots, GPB)) : 0;
+      (p.plan && p.nslots > 0 && !shares) ? std::min(kSegBlocksMax, div_up_host(p.nslots, GPB)) : 0;
+  const int share_blocks =
+      shares ? kXcds * div_up_host(div_up_host(p.nslots, std::min(G, CSRSPMM_SHARE_LANES)), GPB) : 0;
+  constexpr int US = SU > U ? (SU < G ? SU : G) : U;
   int piece_blocks = 0;
   // Column panels reach the float4 kernels and the scalar ones of N > 64
   // (per_call_panels, from N = 128).
@@ -1067,6 +1426,12 @@ hipError_t launch_rg(const Problem& p, hipStream_t s) {
   constexpr int kStaticLds = (LDS ? kWaves * 64 : 1) * (int)sizeof(int2);
   const int pad_lds = cap > 0 ? (kLdsPerCu / cap) / 512 * 512 - kStaticLds : 0;
   for (int s0 = 0; s0 < nslices; s0 += per_launch) {
+    if (share_blocks > 0) {
+      const long long sblocks = (long long)per_launch * share_blocks;
+      if (sblocks > 0x7fffffffLL) return hipErrorInvalidValue;
+      hipLaunchKernelGGL((share_kernel<VEC, G, T, US, LDS, BUF>), dim3((unsigned)sblocks), dim3(kWaves * 64), 0,
+                         s, p, share_blocks, s0);
+    }
     const long long blocks = (long long)piece_blocks + (long long)per_launch * slice_blocks;
     if (blocks == 0) return hipSuccess;
     if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
@@ -1222,21 +1587,35 @@ static hipError_t dispatch_vec1(const Problem& p, hipStream_t s) {
   return dispatch_vec1_cols<LDS, false>(p, s);
 }
 
+// plan_kernel's grid: blocks of 256 rows (grid-strided beyond 4096), and
+// with XCD shares one more block for their column boundaries.
+static int plan_blocks(const Problem& p) {
+  return std::min(div_up_host(p.M + 1, 256), 4096) + (p.shares ? 1 : 0);
+}
+
+hipError_t launch_share_bounds(const Problem& p, hipStream_t s) {
+  const int waves = div_up_host(p.nslots, kShareBoundSlots);
+  if (waves <= 0) return hipSuccess;
+  hipLaunchKernelGGL(share_bounds_kernel, dim3(div_up_host(waves, 4)), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
 hipError_t launch_plan_tables(const Problem& p, hipStream_t s) {
-  const int pblocks = std::min(div_up_host(p.M + 1, 256), 4096);
-  hipLaunchKernelGGL(plan_kernel, dim3(pblocks), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(plan_kernel, dim3(plan_blocks(p)), dim3(256), 0, s, p);
   if (p.dp.P > 0) return launch_panel_schedule(p, s);
   return hipGetLastError();
 }
 
 static hipError_t launch_rowgroup_all(const Problem& p, int vec, bool lds, hipStream_t s) {
-  if (p.plan && !p.plan_ready) {
-    const int pblocks = std::min(div_up_host(p.M + 1, 256), 4096);
-    hipLaunchKernelGGL(plan_kernel, dim3(pblocks), dim3(256), 0, s, p);
-  }
+  if (p.plan && !p.plan_ready) hipLaunchKernelGGL(plan_kernel, dim3(plan_blocks(p)), dim3(256), 0, s, p);
   hipError_t e;
   if (p.dp.P > 0 && !p.dp_ready) {
     e = launch_panel_schedule(p, s);
+    if (e != hipSuccess) return e;
+  }
+  const bool shares = p.plan && p.nslots > 0 && p.shares;
+  if (shares) {
+    e = launch_share_bounds(p, s);
     if (e != hipSuccess) return e;
   }
   if (vec == 4) {
@@ -1245,7 +1624,7 @@ static hipError_t launch_rowgroup_all(const Problem& p, int vec, bool lds, hipSt
     e = lds ? dispatch_vec1<true>(p, s) : dispatch_vec1<false>(p, s);
   }
   if (e != hipSuccess) return e;
-  if (p.plan && ((p.nslots > 0 && !p.no_split) || p.npan > 0 || p.dp.P > 0)) {
+  if (p.plan && ((p.nslots > 0 && !p.no_split) || shares || p.npan > 0 || p.dp.P > 0)) {
     if (vec == 4) {
       launch_combine<4>(p, s);
     } else {

@@ -423,7 +423,62 @@ struct Problem {
   // The caller's max_row_nnz hint (or a stored plan's true longest row);
   // -1 when unknown.
   int row_hint;
+  // XCD shares (share_applies; false: off): long rows are summed XCD by XCD
+  // (see kShareSplitSegs); shr_cb holds the column boundaries (plan_kernel),
+  // shr_pb the per-slot share entries (share_bounds_kernel), both written
+  // each call, shr_part the parts' partial rows.
+  bool shares;
+  int* shr_cb;
+  int4* shr_pb;
+  float* shr_part;
 };
+
+// XCD shares.  On a B far larger than the L2s, with no column panels (hot
+// columns spread over the whole index range, as in R-MAT, or rows too short
+// for panels), every XCD gathers from all of B and its 4 MiB L2 keeps little.
+// Instead, the columns are cut into kXcds ranges at boundaries chosen per call
+// so that each range carries about 1/kXcds of a column sample, and the long
+// rows' nonzeros of range x are summed on XCD x (block b runs on XCD
+// b mod kXcds): each L2 then serves 1/kXcds of the columns.  Measured with an
+// LRU model of the eight L2s over R-MAT N = 64 (16.1 M nonzeros): hit rate
+// 0.39 -> 0.65, L2 misses 2.66 -> 1.52 GB; the model gave 0.39 for the
+// unsplit call, as the hardware counters do.
+//
+//  * A long row of fewer than kShareSplitSegs segments (under 2048
+//    nonzeros) is split: its part x, the nonzeros whose column lies in
+//    range x (for a sorted row, a contiguous run), is summed on XCD x into
+//    shr_part row (rowptr[r] >> kShareIdxShift) + x, written (zero when
+//    empty) for every x, and the combine adds the row's kXcds consecutive
+//    partial rows in order.  Such a row owns the rows
+//    [rowptr[r] >> 4, rowptr[r+1] >> 4), at least floor(len / 16) >= kXcds
+//    of them (len > 128), so the rows of all split rows tile the buffer
+//    without a scan.
+//  * A longer row keeps its segments whole, each summed on the XCD whose
+//    range holds the column at the segment's middle, into the ordinary
+//    segment partials: its segments are narrow in column space, and
+//    splitting them would only multiply its partials by kXcds.
+//
+// The parts of a segment partition its positions whatever the boundaries,
+// so the results never depend on them, only the locality does.
+constexpr int kShareIdxShift = 4;
+constexpr int kShareSplitSegs = 8;
+constexpr int kShareSamples = 4096;      // columns sampled for the boundaries
+constexpr int kShareBins = 1024;         // histogram bins of the sample
+constexpr long long kShareMinBand = 64LL << 20;  // bytes of B (one column slice) from which to split
+constexpr int kShareMinNnz = 1 << 20;
+static_assert(kXcds == 8, "a slot's part offsets are 8 ints");
+
+// The call splits its long rows by XCD: the plan on, no per-call column
+// panels, a B (or column slice of it) of at least kShareMinBand, rows that
+// can be long under the hint, and segments of at least 128 nonzeros (the
+// partial numbering above).
+inline bool share_applies(bool plan, int K, int N, int nnz, int sw, int P, int hint) {
+  if (!plan || P > 0 || nnz < kShareMinNnz || K <= 0) return false;
+  const SegGeom g = seg_geom(nnz);
+  if (g.seg_shift < 7 || g.long_row < 128) return false;
+  if (hint >= 0 && hint <= g.long_row) return false;
+  return (long long)K * (sw > 0 ? sw : N) * 4 >= kShareMinBand;
+}
 
 // Band sweep (sliced float4 calls).  Each group keeps kSweepRows rows'
 // accumulators in registers while all groups walk the slice's band of B in
@@ -501,8 +556,11 @@ struct WorkspaceLayout {
   int nslots, nblocks;
   long long ldp;
   int P, wshift, nwin, nl_max;
+  // XCD shares (after the base sections; panels and shares exclude each other)
+  bool shares;
+  size_t shr_cb_off, shr_pb_off, shr_part_off;
 };
-WorkspaceLayout workspace_layout(int M, int K, int N, int nnz, int P);
+WorkspaceLayout workspace_layout(int M, int K, int N, int nnz, int P, bool shares = false);
 
 // Panels the per-call path uses for this problem (0: none): float4 columns
 // (or scalar ones from N = kPanelMinScalarN), the plan on, and a row of
@@ -533,6 +591,13 @@ hipError_t launch_rowgroup(const Problem& p, int vec, bool lds, hipStream_t s);
 // and dp_flag, find the panel boundaries of the long rows, then compact the
 // panelized rows and deal the panels to the XCDs.
 hipError_t launch_panel_schedule(const Problem& p, hipStream_t s);
+
+// XCD shares: after plan_kernel has written the column boundaries and the
+// segment slots, record where each XCD's part of every split row begins and
+// which XCD sums each segment kept whole.
+hipError_t launch_share_bounds(const Problem& p, hipStream_t s);
+
+
 
 // The tables of a planned call without the product: plan_kernel and, with
 // column panels, the panel schedule (stored plans build them once).

@@ -119,8 +119,23 @@ size_t csrspmm_workspace_bytes(int algo, int M, int N, int nnz);
  * csrspmm_workspace_bytes but less than this size runs without panels.
  * A hint in [0, 256] on fewer than 2^20 rows + nonzeros and 32768 rows, when
  * B is not cut into column slices, gives 0: such a call runs as one launch
- * with no plan and no workspace. */
+ * with no plan and no workspace.  It also holds the XCD share tables and
+ * partial sums (csrspmm_call_shares: (nnz / 16) x N floats) of a call that
+ * splits its long rows by XCD; a smaller workspace of at least
+ * csrspmm_workspace_bytes runs without them. */
 size_t csrspmm_workspace_bytes_ex(int algo, int M, int K, int N, int nnz, int max_row_nnz_hint);
+
+/* 1 when a per-call product of this shape, given a workspace of
+ * csrspmm_workspace_bytes_ex bytes and 16-byte aligned B and C rows, splits
+ * its long rows (above 128 nonzeros) by XCD, else 0.  Such a call cuts each
+ * long-row segment at eight column ranges chosen from a sample of the
+ * columns, sums the part of range x on XCD x, and adds the parts in range
+ * order: within the 1e-5 bar, but no longer the CSR order of the fp32
+ * restatement for those rows.  It applies with the plan on, no column
+ * panels, nnz >= 2^20 and a B (or 64-column slice of it) of at least
+ * 64 MiB, unless the hint rules out rows above 128.  For tests and tuning;
+ * no counterpart in the reference, whose kernels sum each row on one warp. */
+int csrspmm_call_shares(int algo, int M, int K, int N, int nnz, int max_row_nnz_hint);
 
 /* Where a per-call workspace of csrspmm_workspace_bytes_ex bytes holds the
  * call's column-panel decision, for tests and tuning: returns the number of

@@ -4,12 +4,16 @@ documented rule for which rows it sums whole."""
 import numpy as np
 
 
-def whole_row_max(nnz):
+def whole_row_max(nnz, shares=False):
     """Longest row the warp-per-row family sums in one piece (in CSR order,
     so bit-identical to the fp32 restatement) for a matrix of nnz nonzeros:
     rows shorter than two segments.  The segment is 256 nonzeros, halved
     (down to 32) while the matrix holds fewer than 4096 segments' worth, so
-    that a small matrix's long rows still split over the GPU."""
+    that a small matrix's long rows still split over the GPU.  A call that
+    splits its long rows by XCD (shares, capi.call_shares) sums only rows
+    of at most 128 nonzeros whole."""
+    if shares:
+        return 128
     seg = 256
     while seg > 32 and nnz // seg < 4096:
         seg //= 2
@@ -46,3 +50,13 @@ def mixed_lengths(seed, M=3000):
     lens[pos] = special
     lens[-1] = 6000  # a long row at the very end
     return lens
+
+
+def whole_row_limit(algo, rowptr, K, N, hint=-1, shares=None):
+    """whole_row_max for a per-call product of this shape through the
+    library (shares=None: as the library decides, capi.call_shares)."""
+    nnz = int(rowptr[-1])
+    if shares is None:
+        from csrspmm_amd import capi
+        shares = capi.call_shares(algo, int(rowptr.size - 1), int(K), int(N), nnz, hint)
+    return whole_row_max(nnz, shares)

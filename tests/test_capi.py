@@ -223,24 +223,39 @@ def test_csr_tools_argument_errors_without_device():
 def test_workspace_bytes_ex_panels():
     """The panel tables are reserved on a B of >= 16 MiB with N <= 256 (for
     scalar columns from N = 128) when a row of >= 1024 nonzeros is possible
-    under the hint."""
+    under the hint.  Without panels, on a B (or 64-column slice) of >= 64 MiB
+    with 2^20 nonzeros and rows above 128 possible, the XCD share tables and
+    partials ((nnz / 16) x N floats) are reserved instead."""
     lib = capi.hip()
     a = capi.ALGO["WarpPerRowSmemFp4"]
     M, K, N, nnz = 262144, 262144, 128, 8453223
     base = lib.csrspmm_workspace_bytes(a, M, N, nnz)
-    assert lib.csrspmm_workspace_bytes_ex(a, M, K, N, nnz, 1023) == base
-    assert lib.csrspmm_workspace_bytes_ex(a, M, K, N, nnz, 1024) > base
+    share_part = (nnz // 16) * N * 4
     full = lib.csrspmm_workspace_bytes_ex(a, M, K, N, nnz, -1)
     assert full == lib.csrspmm_workspace_bytes_ex(a, M, K, N, nnz, 16384) > base
+    assert lib.csrspmm_workspace_bytes_ex(a, M, K, N, nnz, 1024) == full
     # partials at most 256 MiB, plus tables of a few MiB
     assert full - base <= (256 << 20) + (8 << 20)
+    assert not lib.csrspmm_call_shares(a, M, K, N, nnz, -1)  # panels
+    # below 1024 no panels: the long rows (above 128) are split by XCD
+    assert lib.csrspmm_call_shares(a, M, K, N, nnz, 1023)
+    sh = lib.csrspmm_workspace_bytes_ex(a, M, K, N, nnz, 1023)
+    assert share_part <= sh - base <= share_part + (8 << 20)
+    assert lib.csrspmm_workspace_bytes_ex(a, M, K, N, nnz, 128) == base  # no long rows at all
+    assert not lib.csrspmm_call_shares(a, M, K, N, nnz, 128)
     s = capi.ALGO["WarpPerRowSmem"]
     assert lib.csrspmm_workspace_bytes_ex(s, M, K, N, nnz, -1) > lib.csrspmm_workspace_bytes(s, M, N, nnz)
-    assert lib.csrspmm_workspace_bytes_ex(s, M, K, 64, nnz, -1) == lib.csrspmm_workspace_bytes(s, M, 64, nnz)
+    # scalar columns below N = 128 take no panels: shares on a 64 MiB B
+    assert lib.csrspmm_call_shares(s, M, K, 64, nnz, -1)
+    assert lib.csrspmm_workspace_bytes_ex(s, M, K, 64, nnz, -1) > lib.csrspmm_workspace_bytes(s, M, 64, nnz)
+    assert not lib.csrspmm_call_shares(s, M, K // 2, 64, nnz, -1)  # a 32 MiB B: neither
+    assert lib.csrspmm_workspace_bytes_ex(s, M, K // 2, 64, nnz, -1) == lib.csrspmm_workspace_bytes(s, M, 64, nnz)
     assert lib.csrspmm_workspace_bytes_ex(a, M, K, 64, nnz, -1) > lib.csrspmm_workspace_bytes(a, M, 64, nnz)
     assert lib.csrspmm_workspace_bytes_ex(a, M, 1024, N, nnz, -1) == base  # B of 512 KiB
-    assert lib.csrspmm_workspace_bytes_ex(a, M, K, 512, nnz, -1) == lib.csrspmm_workspace_bytes(a, M, 512, nnz)
     assert lib.csrspmm_workspace_bytes_ex(capi.ALGO["Naive"], M, K, N, nnz, -1) == 0
+    assert not lib.csrspmm_call_shares(capi.ALGO["Naive"], M, K, N, nnz, -1)
+    # too few nonzeros for the shares
+    assert not lib.csrspmm_call_shares(s, M, K, 64, (1 << 20) - 1, -1)
 
 
 def test_panel_rules_without_device():

@@ -17,7 +17,7 @@ import torch
 
 import oracle
 from csrspmm_amd import ALGORITHMS, capi, gen
-from csr_cases import csr_from_lengths, mixed_lengths, whole_row_max
+from csr_cases import csr_from_lengths, mixed_lengths, whole_row_limit, whole_row_max
 
 pytestmark = pytest.mark.gpu
 
@@ -58,7 +58,7 @@ def check(algo, C, rowptr, colidx, vals, B, C0=None, alpha=1.0, beta=0.0, what="
     bad, ratio, _, _ = oracle.check(C, R, S, TOL)
     assert bad == 0, f"{algo} {what}: {bad} elements off (max ratio {ratio:.3g})"
     F = oracle.spmm_f32_seq(rowptr, colidx, vals, B, C0, alpha, beta)
-    whole = np.diff(rowptr) <= whole_row_max(int(rowptr[-1]))
+    whole = np.diff(rowptr) <= whole_row_limit(algo, rowptr, B.shape[0], B.shape[1])
     assert np.array_equal(C[whole].view(np.uint32), F[whole].view(np.uint32)), \
         f"{algo} {what}: short rows differ from the fp32 restatement"
 

@@ -24,7 +24,7 @@ import torch
 
 import oracle
 from csrspmm_amd import ALGORITHMS, capi, configs, gen
-from csr_cases import csr_from_lengths, whole_row_max
+from csr_cases import csr_from_lengths, whole_row_limit, whole_row_max
 from golden_cases import load, names
 
 pytestmark = pytest.mark.gpu
@@ -57,7 +57,7 @@ def run_spmm(algo, rowptr, colidx, vals, B, dev, C0=None, alpha=1.0, beta=0.0, h
 
 
 def assert_parity(algo, C, rowptr, colidx, vals, B, C0, alpha, beta, rows=None, c0_zero=False,
-                  what=""):
+                  what="", hint=-1, shares=None):
     R, S = oracle.spmm_f64(rowptr, colidx, vals, B, C0, alpha, beta, c0_zero=c0_zero, rows=rows)
     Cs = C if rows is None else C[rows]
     bad, ratio, plain, worst = oracle.check(Cs, R, S, TOL)
@@ -67,7 +67,7 @@ def assert_parity(algo, C, rowptr, colidx, vals, B, C0, alpha, beta, rows=None, 
     ridx = np.arange(rowptr.size - 1) if rows is None else np.asarray(rows)
     lens = rowptr[ridx + 1] - rowptr[ridx]
     whole = (np.ones_like(lens, dtype=bool) if algo in WHOLE_ROW_ALGOS
-             else lens <= whole_row_max(int(rowptr[-1])))
+             else lens <= whole_row_limit(algo, rowptr, B.shape[0], B.shape[1], hint, shares))
     a = Cs[whole].view(np.uint32)
     b = F[whole].view(np.uint32)
     # +0 and -0 only differ in sign bits; NaN payloads are not compared.
@@ -133,7 +133,7 @@ def test_xl_deterministic_and_hint_independent(gpu):
     C3 = run_spmm("WarpPerRowSmemFp4", a.rowptr, a.colidx, a.vals, B, gpu, hint=8)
     rows = sample_rows(a, False)
     assert_parity("WarpPerRowSmemFp4", C3, a.rowptr, a.colidx, a.vals, B, None, 1.0, 0.0,
-                  rows=rows, what="xl hint=8")
+                  rows=rows, what="xl hint=8", hint=8)
     # the library-owned workspace path gives the same bits
     C4 = run_spmm("WarpPerRowFp4", a.rowptr, a.colidx, a.vals, B, gpu, owned=True)
     assert np.array_equal(C1.view(np.uint32), C4.view(np.uint32))
@@ -208,10 +208,10 @@ def test_row_hint(algo, hint, gpu):
     vals = rng.uniform(-1, 1, colidx.size).astype(np.float32)
     B = rng.uniform(-1, 1, (K, 64)).astype(np.float32)
     C = run_spmm(algo, rowptr, colidx, vals, B, gpu, hint=hint)
-    assert_parity(algo, C, rowptr, colidx, vals, B, None, 1.0, 0.0, what=f"hint={hint}")
+    assert_parity(algo, C, rowptr, colidx, vals, B, None, 1.0, 0.0, what=f"hint={hint}", hint=hint)
     C0 = rng.uniform(-1, 1, (lens.size, 64)).astype(np.float32)
     C = run_spmm(algo, rowptr, colidx, vals, B, gpu, C0=C0, alpha=0.5, beta=2.0, hint=hint)
-    assert_parity(algo, C, rowptr, colidx, vals, B, C0, 0.5, 2.0, what=f"hint={hint} beta")
+    assert_parity(algo, C, rowptr, colidx, vals, B, C0, 0.5, 2.0, what=f"hint={hint} beta", hint=hint)
 
 
 @functools.lru_cache(maxsize=None)
@@ -241,11 +241,11 @@ def test_hinted_short_rows_one_launch(algo, shape, gpu):
         assert capi.hip().csrspmm_workspace_bytes_ex(capi.ALGO[algo], M, K, N, colidx.size, hint) == 0
         print(f"[parity] one launch {algo} M={M} K={K} N={N} hint={hint}", flush=True)
         C = run_spmm(algo, rowptr, colidx, vals, B, gpu, hint=hint)
-        assert_parity(algo, C, rowptr, colidx, vals, B, None, 1.0, 0.0, what=f"hint={hint}")
+        assert_parity(algo, C, rowptr, colidx, vals, B, None, 1.0, 0.0, what=f"hint={hint}", hint=hint)
         F = oracle.spmm_f32_seq(rowptr, colidx, vals, B, None, 1.0, 0.0)
         assert np.array_equal(C.view(np.uint32), F.view(np.uint32)), "rows summed whole"
     C = run_spmm(algo, rowptr, colidx, vals, B, gpu, C0=C0, alpha=0.5, beta=-1.5, hint=int(lens.max()))
-    assert_parity(algo, C, rowptr, colidx, vals, B, C0, 0.5, -1.5, what="beta")
+    assert_parity(algo, C, rowptr, colidx, vals, B, C0, 0.5, -1.5, what="beta", hint=int(lens.max()))
 
 
 @pytest.mark.parametrize("algo", ALGORITHMS)

@@ -37,7 +37,7 @@ def test_plan_configs(cfg_name, algo, gpu):
     C1 = plan_run(plan, B, gpu, a.M, cfg.N)
     assert not np.isnan(C1).any()
     assert_parity(concrete, C1, a.rowptr, a.colidx, a.vals, B, None, 1.0, 0.0, rows=rows,
-                  what=f"plan {cfg_name}")
+                  what=f"plan {cfg_name}", shares=False)
     C2 = plan_run(plan, B, gpu, a.M, cfg.N)
     assert np.array_equal(C1.view(np.uint32), C2.view(np.uint32))  # deterministic, reusable
     if cfg_name == "xl":
@@ -60,10 +60,10 @@ def test_plan_epilogues_and_growth(gpu):
         rows = sample_rows(a, False)
         C = plan_run(plan, B, gpu, a.M, N, C0=C0, alpha=0.5, beta=-2.0)
         assert_parity(plan.algorithm, C, a.rowptr, a.colidx, a.vals, B, C0, 0.5, -2.0, rows=rows,
-                      what=f"plan beta N={N}")
+                      what=f"plan beta N={N}", shares=False)
         C = plan_run(plan, B, gpu, a.M, N, alpha=1.5, beta=0.25, flags=capi.FLAG_C_IS_ZERO)
         assert_parity(plan.algorithm, C, a.rowptr, a.colidx, a.vals, B, None, 1.5, 0.25,
-                      rows=rows, c0_zero=True, what=f"plan c_is_zero N={N}")
+                      rows=rows, c0_zero=True, what=f"plan c_is_zero N={N}", shares=False)
     plan.close()
 
 
@@ -82,7 +82,7 @@ def test_plan_unsorted_long_rows_and_small_matrix(gpu):
                      n_hint=64)
     assert plan.panelized_rows == 2
     C = plan_run(plan, B, gpu, lens.size, 64)
-    assert_parity("WarpPerRowFp4", C, rowptr, colidx, vals, B, None, 1.0, 0.0, what="unsorted")
+    assert_parity("WarpPerRowFp4", C, rowptr, colidx, vals, B, None, 1.0, 0.0, what="unsorted", shares=False)
     plan.close()
     # tiny matrix: no stored structures, still correct
     b = gen.ragged(50, 40, 0, 20, seed=2)
@@ -90,7 +90,7 @@ def test_plan_unsorted_long_rows_and_small_matrix(gpu):
     plan = capi.Plan("Auto", dev_t(b.rowptr, gpu), dev_t(b.colidx, gpu), dev_t(b.vals, gpu), 40,
                      n_hint=8)
     C = plan_run(plan, Bs, gpu, 50, 8)
-    assert_parity(plan.algorithm, C, b.rowptr, b.colidx, b.vals, Bs, None, 1.0, 0.0, what="tiny")
+    assert_parity(plan.algorithm, C, b.rowptr, b.colidx, b.vals, Bs, None, 1.0, 0.0, what="tiny", shares=False)
     plan.close()
 
 
@@ -135,4 +135,4 @@ def test_auto_takes_scalar_lds_on_l2_sized_long_rows(gpu):
     C_plan = plan_run(plan, B, gpu, M, N)
     plan.close()
     assert_parity("WarpPerRowSmem", C_plan, a.rowptr, a.colidx, a.vals, B, None, 1.0, 0.0,
-                  rows=np.arange(0, M, 7), what="auto shape rule, plan")
+                  rows=np.arange(0, M, 7), what="auto shape rule, plan", shares=False)

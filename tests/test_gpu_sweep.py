@@ -157,8 +157,11 @@ def test_sweep_wide_band_with_hint(gpu):
     """A 64-column band wider than 16 MiB (K = 81920: 20 MiB) is sliced only
     when the call sweeps with at least 4 nonzeros per band and no column
     panels can apply, as with a max_row_nnz hint below 1024.  Checked against
-    the oracle and, bit for bit, against the scalar-column variant, which
-    stays unsliced there, and the LDS-staged float4 variant, which sweeps."""
+    the oracle and, bit for bit, against the LDS-staged float4 variant, which
+    sweeps too, and the scalar-column variant, which stays unsliced there:
+    on its 80 MiB B it splits the long rows by XCD (capi.call_shares), so
+    against it only rows of at most 128 nonzeros, summed whole by both, are
+    compared bit for bit."""
     M, K, N = MS, 81920, 256
     rp, ci, va = rows_csr(lengths_for(M, 18, ((3, 300), (MS - 1, 700))), K, 19, (8,))
     rng = np.random.default_rng(20)
@@ -167,8 +170,15 @@ def test_sweep_wide_band_with_hint(gpu):
     h = int(np.diff(rp).max())
     C = run("WarpPerRowFp4", gpu, rp, ci, va, B, C0, -1.25, 0.5, hint=h)
     check_all(C.cpu().numpy(), rp, ci, va, B, -1.25, 0.5, C0, "wide band")
+    assert not capi.call_shares("WarpPerRowFp4", M, K, N, int(va.size), h)
     for other in ("WarpPerRow", "WarpPerRowSmemFp4"):
-        assert torch.equal(C, run(other, gpu, rp, ci, va, B, C0, -1.25, 0.5, hint=h)), other
+        Co = run(other, gpu, rp, ci, va, B, C0, -1.25, 0.5, hint=h)
+        if capi.call_shares(other, M, K, N, int(va.size), h):
+            check_all(Co.cpu().numpy(), rp, ci, va, B, -1.25, 0.5, C0, f"wide band {other}")
+            short = torch.from_numpy(np.diff(rp) <= 128).to(gpu)
+            assert torch.equal(C[short], Co[short]), other
+        else:
+            assert torch.equal(C, Co), other
 
 
 @pytest.mark.parametrize("N", [128, 64])
