@@ -254,7 +254,31 @@ static bool sliced(int M, int K, int N, int nnz, int hint) {
   return slice_width(K, N, P > 0, wide_sweep(4, plan, M, K, nnz)) > 0;
 }
 
+// A float4 call from N = 128 cut into column slices that are not swept, or
+// swept with fewer than kSweepWideMinPerBand nonzeros per band and row, and
+// whose long rows are split by XCD (share_applies).
+static bool sliced_shares(int M, int K, int N, int nnz, int hint) {
+  const bool plan = wants_plan(CSRSPMM_ALGO_WARP_PER_ROW_FP4, M, K, N, nnz, hint);
+  if (!plan) return false;
+  const int P = per_call_panels(4, plan, K, N, nnz, hint);
+  const int sw = slice_width(K, N, P > 0, wide_sweep(4, plan, M, K, nnz));
+  return sw > 0 && !sweep_applies(plan, M, K, nnz, sw, kSweepWideMinPerBand) &&
+         share_applies(plan, K, N, nnz, sw, 0, hint);
+}
+
 int resolve_algorithm(int algo, int M, int K, int N, int nnz, int hint) {
+  if (algo == CSRSPMM_ALGO_AUTO && N % 4 == 0 && N >= 128 && sliced_shares(M, K, N, nnz, hint)) {
+    // Column slices that are not swept (or swept with under 4 nonzeros per
+    // band), of a matrix whose long rows are split by XCD: the scalar
+    // LDS-staged form's 64-lane groups (a slice's 64 columns, one per lane)
+    // run four times the waves of the float4 16-lane groups over the short
+    // rows and the parts.  Measured on MI355X per call without a hint: R-MAT
+    // N = 512 4218 -> 3832 us, N = 256 2156 -> 1886; uniform rows of 16
+    // (524288 x 262144) at N = 512 2614 -> 2592; swept with 2 per band,
+    // power-law rows (mean 32, 262144^2) at N = 1024 7021 -> 5197 and uniform
+    // rows of 32 (262144^2) at N = 1024 5811 -> 4874.
+    return CSRSPMM_ALGO_WARP_PER_ROW_SMEM;
+  }
   if (algo == CSRSPMM_ALGO_AUTO && N % 4 == 0 && N >= 128 && M > 0 && hint > kLongRow &&
       (long long)hint > 4LL * nnz / M && sliced(M, K, N, nnz, hint)) {
     // Column slices of skewed rows (the hint above both long_row and 4x the

@@ -83,6 +83,10 @@ int csrspmm_resolve_algorithm(int algo, int N);
 /* The concrete variant CSRSPMM_ALGO_AUTO runs for the whole shape (A is
  * M x K with nnz nonzeros, N output columns, max_row_nnz_hint as for the
  * SpMM, -1 if unknown): csrspmm_resolve_algorithm's choice, except that
+ *  - from N = 128 (N % 4 == 0), a call cut into column slices that are not
+ *    swept, or swept with fewer than 4 nonzeros per band and row, whose
+ *    long rows are split by XCD (csrspmm_call_shares for the float4
+ *    variant), takes the scalar LDS-staged variant;
  *  - below N = 128 (N % 4 == 0), rows of 24 or more nonzeros on average
  *    with per-call column panels possible for float4 columns (a B of at
  *    least 64 MiB, a row of 1024 or more not ruled out) take the float4

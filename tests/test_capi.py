@@ -76,6 +76,14 @@ def test_parse_and_names():
     assert ex(6, 1 << 20, 1 << 20, 64, 16 << 20) == 4       # R-MAT-like: 16 per row
     assert ex(6, 262144, 262144, 66, 8453223) == 4          # N % 4 != 0
     assert ex(6, 4096, 4096, 64, 4096 * 200) == 4           # small B: scalar
+    # from N = 128, sliced calls split by XCD (not swept) take the scalar
+    # LDS-staged variant: R-MAT at N = 256 and 512, K = 262144 at N = 1024
+    # (or swept with under 4 nonzeros per band)
+    assert ex(6, 1 << 20, 1 << 20, 256, 16 << 20) == 4
+    assert lib.csrspmm_call_shares(3, 1 << 20, 1 << 20, 512, 16 << 20, -1) == 1
+    assert ex(6, 1 << 20, 1 << 20, 128, 16 << 20) == 3      # N = 128: panels, no slices
+    assert ex(6, 262144, 262144, 1024, 8453223) == 4        # XL at N = 1024: 2 per band
+    assert ex(6, 262144, 262144, 1024, 262144 * 64) == 5    # 4 per band: the sweep
     # from N = 128, swept column slices take the float4 LDS-staged variant
     assert ex(6, 65536, 65536, 256, 4325376) == 5           # large
     assert ex(6, 65536, 65536, 256, 65536 * 7) == 3         # under 2 per band: merge blocks
@@ -90,7 +98,7 @@ def test_parse_and_names():
     assert ex(6, 8192, 65536, 256, 8192 * 300, 300) == 3
     assert ex(6, 4096, 65536, 128, 4096 * 512) == 3          # 512 per row: split rows
     assert ex(6, 4096, 65536, 128, 4096 * 63) == 3
-    assert ex(6, 1 << 20, 1 << 20, 512, 16 << 20) == 3      # R-MAT N = 512: 0.25 per band
+    assert ex(6, 1 << 20, 1 << 20, 512, 16 << 20) == 4      # R-MAT N = 512: split by XCD
     # sliced calls of skewed rows (a hint above 128 and 4x the mean) take the scalar LDS form
     assert ex(6, 1 << 20, 1 << 20, 512, 16084813, 39531) == 4   # R-MAT N = 512 with its hint
     assert ex(6, 65536, 65536, 256, 65536 * 32, 16384) == 4     # power-law rows, even swept
