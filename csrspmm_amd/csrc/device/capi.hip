@@ -5,7 +5,9 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <thread>
 #include <string.h>
@@ -137,12 +139,14 @@ int to_status(hipError_t e) { return e == hipSuccess ? 0 : (int)e; }
 // per thread as well.  The map holds at most kMaxOwnedWorkspaces entries; a
 // new key beyond that evicts the least recently used one.
 //
-// Threading: g_ws_mutex is held from the lookup until the call's kernels are
-// enqueued (spmm_impl), so a buffer is never freed between the moment a
-// call takes it and the moment its kernels are queued behind it.  Growing a
-// buffer synchronises its stream first (the stream is alive: its caller is
-// using it); evicting or releasing one synchronises the whole device, since
-// the stream it was keyed on may have been destroyed since.
+// Threading: every workspace has its own lock, held from the moment a call
+// takes it until the call's kernels are enqueued (spmm_impl), so a buffer is
+// never freed or regrown between a call taking it and its kernels being
+// queued behind it.  Calls on different streams or devices share only
+// g_ws_mutex, for the map lookup, not across the enqueue.  Growing a buffer
+// synchronises its stream first (the stream is alive: its caller is using
+// it); evicting or releasing one takes its lock and synchronises the whole
+// device, since the stream it was keyed on may have been destroyed since.
 struct WsKey {
   int dev;
   void* stream;
@@ -155,15 +159,17 @@ struct WsKey {
 };
 
 struct OwnedWorkspace {
-  void* ptr = nullptr;
+  std::mutex m;
+  void* ptr = nullptr;     // ptr, bytes, dead: under m
   size_t bytes = 0;
-  unsigned long long last_use = 0;
+  bool dead = false;       // released or evicted: look it up again
+  unsigned long long last_use = 0;  // under g_ws_mutex
 };
 
 constexpr size_t kMaxOwnedWorkspaces = 16;
 
 std::mutex g_ws_mutex;
-std::map<WsKey, OwnedWorkspace> g_ws;
+std::map<WsKey, std::shared_ptr<OwnedWorkspace>> g_ws;
 unsigned long long g_ws_clock = 0;
 
 WsKey ws_key(int dev, void* stream) {
@@ -173,8 +179,9 @@ WsKey ws_key(int dev, void* stream) {
 }
 
 // Frees one workspace after all work on its device has finished.  Caller
-// holds g_ws_mutex.
+// holds w.m.
 int free_owned_device_synced(int dev, OwnedWorkspace& w) {
+  w.dead = true;
   if (!w.ptr) return 0;
   int cur = 0;
   hipError_t e = hipGetDevice(&cur);
@@ -190,27 +197,42 @@ int free_owned_device_synced(int dev, OwnedWorkspace& w) {
   return (int)e3;
 }
 
-// The workspace of (current device, stream), grown to at least `bytes`.
-// Caller holds g_ws_mutex until the kernels that use it are enqueued.
-int owned_workspace_locked(void* stream, size_t bytes, void** out) {
+// The workspace of (current device, stream), grown to at least `bytes`, in
+// *out; it stays locked through `lock` (and alive through `held`) until the
+// caller has enqueued the kernels that use it.
+int owned_workspace(void* stream, size_t bytes, void** out, std::shared_ptr<OwnedWorkspace>& held,
+                    std::unique_lock<std::mutex>& lock) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return (int)e;
   const WsKey key = ws_key(dev, stream);
-  auto it = g_ws.find(key);
-  if (it == g_ws.end()) {
-    if (g_ws.size() >= kMaxOwnedWorkspaces) {
-      auto lru = g_ws.begin();
-      for (auto j = g_ws.begin(); j != g_ws.end(); ++j)
-        if (j->second.last_use < lru->second.last_use) lru = j;
-      const int st = free_owned_device_synced(lru->first.dev, lru->second);
-      g_ws.erase(lru);
-      if (st != 0) return st;
+  for (;;) {
+    {
+      std::lock_guard<std::mutex> g(g_ws_mutex);
+      auto it = g_ws.find(key);
+      if (it == g_ws.end()) {
+        if (g_ws.size() >= kMaxOwnedWorkspaces) {
+          auto lru = g_ws.begin();
+          for (auto j = g_ws.begin(); j != g_ws.end(); ++j)
+            if (j->second->last_use < lru->second->last_use) lru = j;
+          const std::shared_ptr<OwnedWorkspace> victim = lru->second;
+          const int vdev = lru->first.dev;
+          g_ws.erase(lru);
+          // a call holding the victim's lock never waits for g_ws_mutex
+          std::lock_guard<std::mutex> vl(victim->m);
+          const int st = free_owned_device_synced(vdev, *victim);
+          if (st != 0) return st;
+        }
+        it = g_ws.emplace(key, std::make_shared<OwnedWorkspace>()).first;
+      }
+      held = it->second;
+      held->last_use = ++g_ws_clock;
     }
-    it = g_ws.emplace(key, OwnedWorkspace{}).first;
+    lock = std::unique_lock<std::mutex>(held->m);
+    if (!held->dead) break;
+    lock.unlock();  // evicted or released between the lookup and the lock
   }
-  OwnedWorkspace& w = it->second;
-  w.last_use = ++g_ws_clock;
+  OwnedWorkspace& w = *held;
   if (w.bytes < bytes) {
     if (w.ptr) {
       e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
@@ -480,7 +502,8 @@ int spmm_impl(int algo_in, int M, int K, int N, int nnz, const int* rowptr, cons
   if (st != 0) return st;
   if (M == 0 || N == 0) return 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // held (owned workspaces only) until the kernels are enqueued
+  // an owned workspace stays locked until the kernels are enqueued
+  std::shared_ptr<OwnedWorkspace> held;
   std::unique_lock<std::mutex> lock;
   p.plan = wants_plan(algo, M, K, N, nnz, hint);
   if (p.plan) {
@@ -491,12 +514,11 @@ int spmm_impl(int algo_in, int M, int K, int N, int nnz, const int* rowptr, cons
     if (p.sw > 0) P = 0;  // a sliced call gathers band by band instead
     WorkspaceLayout L = workspace_layout(M, K, N, nnz, P, share_applies(true, K, N, nnz, p.sw, P, hint));
     if (owned) {
-      lock = std::unique_lock<std::mutex>(g_ws_mutex);
-      st = owned_workspace_locked(stream, L.total, &ws);
+      st = owned_workspace(stream, L.total, &ws, held, lock);
       if (st == CSRSPMM_STATUS_ALLOC_FAILED && L.total > L.base_total) {
         // no room for the panel or share tables: run without them
         L = workspace_layout(M, K, N, nnz, 0);
-        st = owned_workspace_locked(stream, L.total, &ws);
+        st = owned_workspace(stream, L.total, &ws, held, lock);
       }
       if (st != 0) return st;
     } else {
@@ -559,19 +581,21 @@ __global__ void zero2_kernel(int* out) {
 
 // Timing hook state: a pool of event pairs; pairs [0, g_t_used) hold
 // recordings not yet read.
-std::mutex g_t_mutex;
-bool g_t_on = false;
+std::mutex g_t_mutex;                // the event pool
+std::atomic<bool> g_t_on{false};     // read without the lock on every call
 std::vector<std::pair<hipEvent_t, hipEvent_t>> g_t_events;
 size_t g_t_used = 0;
 
 }  // namespace
 
 thread_local int t_timing_depth = 0;
+thread_local bool t_timing_recorded = false;  // the outermost call recorded a start event
 
 void timing_before_main(hipStream_t s) {
   if (t_timing_depth++ > 0) return;
+  t_timing_recorded = false;
+  if (!g_t_on.load(std::memory_order_relaxed)) return;
   std::lock_guard<std::mutex> lock(g_t_mutex);
-  if (!g_t_on) return;
   if (g_t_used == g_t_events.size()) {
     hipEvent_t a, b;
     if (hipEventCreate(&a) != hipSuccess) return;
@@ -581,13 +605,14 @@ void timing_before_main(hipStream_t s) {
     }
     g_t_events.emplace_back(a, b);
   }
-  (void)hipEventRecord(g_t_events[g_t_used].first, s);
+  t_timing_recorded = hipEventRecord(g_t_events[g_t_used].first, s) == hipSuccess;
 }
 
 void timing_after_main(hipStream_t s) {
-  if (--t_timing_depth > 0) return;
+  if (--t_timing_depth > 0 || !t_timing_recorded) return;
+  t_timing_recorded = false;
   std::lock_guard<std::mutex> lock(g_t_mutex);
-  if (!g_t_on || g_t_used == g_t_events.size()) return;
+  if (g_t_used == g_t_events.size()) return;
   (void)hipEventRecord(g_t_events[g_t_used].second, s);
   ++g_t_used;
 }
@@ -711,10 +736,15 @@ int csrspmm_spmm_f32_noalloc(int algo, int M, int K, int N, int nnz, const int* 
                              const int* colidx, const float* vals, int max_row_nnz_hint,
                              const float* B, long long ldb, float* C, long long ldc, float alpha,
                              float beta, unsigned flags, void* stream) {
-  // The base workspace (block starts, segment slots, partials) must fit; the
-  // per-call panel tables are optional: spmm_impl runs without them when the
-  // scratch cannot hold them, as for any workspace of base size.
-  if (csrspmm_workspace_bytes(algo, M, N, nnz) > CSRSPMM_NOALLOC_SCRATCH_BYTES)
+  // The base workspace (block starts, segment slots, partials) of the call's
+  // own plan must fit, none when it runs without one (a hint can make a
+  // mid-sized call one launch); the per-call panel and share tables are
+  // optional: spmm_impl runs without them when the scratch cannot hold them,
+  // as for any workspace of base size.
+  const int ralgo = resolve_algorithm(algo, M, K, N, nnz, max_row_nnz_hint);
+  if (ralgo >= 0 && M > 0 && N > 0 && nnz >= 0 && K >= 0 &&
+      wants_plan(ralgo, M, K, N, nnz, max_row_nnz_hint) &&
+      workspace_layout(M, K, N, nnz, 0).base_total > CSRSPMM_NOALLOC_SCRATCH_BYTES)
     return CSRSPMM_STATUS_SCRATCH_TOO_SMALL;
   void* ws = nullptr;
   const int st = scratch_on_current_device(&ws);
@@ -727,31 +757,46 @@ int csrspmm_release_workspace(void* stream) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return (int)e;
-  std::lock_guard<std::mutex> lock(g_ws_mutex);
-  auto it = g_ws.find(ws_key(dev, stream));
-  if (it == g_ws.end()) return 0;
+  std::shared_ptr<OwnedWorkspace> w;
+  {
+    std::lock_guard<std::mutex> g(g_ws_mutex);
+    auto it = g_ws.find(ws_key(dev, stream));
+    if (it == g_ws.end()) return 0;
+    w = it->second;
+    g_ws.erase(it);
+  }
+  std::lock_guard<std::mutex> l(w->m);  // after any call still enqueuing on it
+  w->dead = true;
   e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
-  hipError_t e2 = it->second.ptr ? hipFree(it->second.ptr) : hipSuccess;
-  g_ws.erase(it);
+  hipError_t e2 = w->ptr ? hipFree(w->ptr) : hipSuccess;
+  w->ptr = nullptr;
+  w->bytes = 0;
   if (e != hipSuccess) return (int)e;
   return to_status(e2);
 }
 
 int csrspmm_release_all_workspaces(void) {
-  std::lock_guard<std::mutex> lock(g_ws_mutex);
+  std::map<WsKey, std::shared_ptr<OwnedWorkspace>> all;
+  {
+    std::lock_guard<std::mutex> g(g_ws_mutex);
+    all.swap(g_ws);
+  }
   int st = 0;
-  for (auto& kv : g_ws) {
-    const int s1 = free_owned_device_synced(kv.first.dev, kv.second);
+  for (auto& kv : all) {
+    std::lock_guard<std::mutex> l(kv.second->m);
+    const int s1 = free_owned_device_synced(kv.first.dev, *kv.second);
     if (st == 0) st = s1;
   }
-  g_ws.clear();
   return st;
 }
 
 int csrspmm_owned_workspaces(size_t* bytes_out) {
-  std::lock_guard<std::mutex> lock(g_ws_mutex);
+  std::lock_guard<std::mutex> g(g_ws_mutex);
   size_t total = 0;
-  for (const auto& kv : g_ws) total += kv.second.bytes;
+  for (const auto& kv : g_ws) {
+    std::lock_guard<std::mutex> l(kv.second->m);
+    total += kv.second->bytes;
+  }
   if (bytes_out) *bytes_out = total;
   return (int)g_ws.size();
 }
@@ -798,8 +843,7 @@ int csrspmm_stream_synchronize(void* stream) {
 }
 int csrspmm_get_last_error(void) { return to_status(hipGetLastError()); }
 int csrspmm_timing_enable(int on) {
-  std::lock_guard<std::mutex> lock(g_t_mutex);
-  g_t_on = on != 0;
+  g_t_on.store(on != 0, std::memory_order_relaxed);
   return 0;
 }
 

@@ -105,6 +105,7 @@ struct csrspmm_plan_s {
   void* d_ws = nullptr;
   size_t ws_bytes = 0;
   int tab_n = 0, tab_vec = 0, tab_P = -1;
+  bool tab_sliced = false;
   WorkspaceLayout tab_L{};
   int dev_nl = 0;  // rows the device schedule panelized
   // partial buffers, grown with N
@@ -184,6 +185,34 @@ int build_rowgroup_plan(csrspmm_plan_s* p, const std::vector<int>& rp, int n_hin
       if (sorted) pan_rows.push_back(r);
     }
   }
+  // Pieces: (row index i, panel, [a, b)) with b - a <= kPieceMaxLen.
+  struct Piece {
+    int i, a, b;
+  };
+  const long long width = P > 0 ? ((long long)K + P - 1) / P : 1;
+  std::vector<std::vector<Piece>> by_panel((size_t)P);
+  for (int i = 0; i < (int)pan_rows.size(); ++i) {
+    const int r = pan_rows[(size_t)i];
+    int a = rp[r];
+    for (int pn = 0; pn < P; ++pn) {
+      const long long hi_col = (pn + 1) * width;
+      const int b = (int)(std::lower_bound(hcol.begin() + a, hcol.begin() + rp[r + 1], (int)std::min<long long>(hi_col, 0x7fffffff)) - hcol.begin());
+      for (int x = a; x < b; x += kPieceMaxLen)
+        by_panel[(size_t)pn].push_back({i, x, std::min(b, x + kPieceMaxLen)});
+      a = b;
+    }
+  }
+  // Skewed columns (a few hot panels, as in R-MAT graphs) already give L2
+  // reuse without panels, and panels there only add partial traffic: keep
+  // such rows on the ordinary segment path.
+  std::vector<long long> weight((size_t)P, 0);
+  long long total = 0;
+  for (int pn = 0; pn < P; ++pn) {
+    for (const Piece& pc : by_panel[(size_t)pn]) weight[(size_t)pn] += pc.b - pc.a + 1;
+    total += weight[(size_t)pn];
+  }
+  if (total > 0 && *std::max_element(weight.begin(), weight.end()) * P > kPanelSkewMax * total)
+    pan_rows.clear();  // back to segments, before the merge blocks are sized
   std::vector<char> panelized((size_t)M, 0);
   for (int r : pan_rows) panelized[r] = 1;
 
@@ -219,41 +248,6 @@ int build_rowgroup_plan(csrspmm_plan_s* p, const std::vector<int>& rp, int n_hin
   if (e != hipSuccess) return (int)e;
   if (pan_rows.empty()) return 0;
 
-  // Pieces: (row index i, panel, [a, b)) with b - a <= kPieceMaxLen.
-  struct Piece {
-    int i, a, b;
-  };
-  const long long width = ((long long)K + P - 1) / P;
-  std::vector<std::vector<Piece>> by_panel((size_t)P);
-  for (int i = 0; i < (int)pan_rows.size(); ++i) {
-    const int r = pan_rows[(size_t)i];
-    int a = rp[r];
-    for (int pn = 0; pn < P; ++pn) {
-      const long long hi_col = (pn + 1) * width;
-      const int b = (int)(std::lower_bound(hcol.begin() + a, hcol.begin() + rp[r + 1], (int)std::min<long long>(hi_col, 0x7fffffff)) - hcol.begin());
-      for (int x = a; x < b; x += kPieceMaxLen)
-        by_panel[(size_t)pn].push_back({i, x, std::min(b, x + kPieceMaxLen)});
-      a = b;
-    }
-  }
-  // Skewed columns (a few hot panels, as in R-MAT graphs) already give L2
-  // reuse without panels, and panels there only add partial traffic: keep
-  // such rows on the ordinary segment path.
-  std::vector<long long> weight((size_t)P, 0);
-  long long total = 0;
-  for (int pn = 0; pn < P; ++pn) {
-    for (const Piece& pc : by_panel[(size_t)pn]) weight[(size_t)pn] += pc.b - pc.a + 1;
-    total += weight[(size_t)pn];
-  }
-  if (*std::max_element(weight.begin(), weight.end()) * P > kPanelSkewMax * total) {
-    for (int r : pan_rows) {  // back to segments
-      const int s0 = rp[r] >> g.slot_shift;
-      for (int k = 0; k < seg_count(rp[r + 1] - rp[r], g.long_row, g.seg_shift); ++k)
-        seg_info[(size_t)s0 + k] = make_int2(r, k);
-    }
-    return to_status(hipMemcpy(p->d_seg_info, seg_info.data(), seg_info.size() * sizeof(int2),
-                               hipMemcpyHostToDevice));
-  }
   // Panels go to XCDs in column order, each to the XCD with the least work so
   // far; each XCD list keeps its panels in column order and is cut into units
   // of ~kPanelUnitItems.
@@ -337,10 +331,16 @@ int device_panels(const csrspmm_plan_s* p, int vec, int N) {
   return slice_width(p->K, N, P > 0) > 0 ? 0 : P;
 }
 
-// A Problem carrying the plan's CSR and tables for N (B and C are the call's).
+// Column-slice width of a call of N with P panels: the per-call rule.
+int device_slice_width(const csrspmm_plan_s* p, int vec, int N, int P) {
+  return P > 0 ? 0 : slice_width(p->K, N, false, wide_sweep(vec, true, p->M, p->K, p->nnz));
+}
+
+// A Problem carrying the plan's CSR and tables (B and C are the call's); the
+// merge blocks are the per-call path's for the tables' slicing.
 void bind_tables(const csrspmm_plan_s* p, Problem& q, int vec) {
   q.plan = true;
-  bind_workspace(q, p->d_ws, p->tab_L, merge_block(vec, p->M, p->nnz));
+  bind_workspace(q, p->d_ws, p->tab_L, call_merge_block(vec, p->M, p->nnz, p->tab_sliced));
   set_row_hint(q, p->maxlen);
 }
 
@@ -367,6 +367,7 @@ hipError_t build_device_tables(csrspmm_plan_s* p, int N, int vec, hipStream_t s)
   p->tab_n = N;
   p->tab_vec = vec;
   p->tab_P = P;
+  p->tab_sliced = device_slice_width(p, vec, N, P) > 0;
   Problem q{};
   q.M = p->M;
   q.K = p->K;
@@ -475,17 +476,16 @@ int csrspmm_plan_spmm_f32(csrspmm_plan_t plan, int N, const float* B, long long 
     // panels, column width or partial width differ from theirs
     const int vec = vector_width(p->algo, pr);
     const int P = device_panels(p, vec, N);
+    const int sw = device_slice_width(p, vec, N, P);
     const long long ldp = ((long long)N + 3) & ~3LL;
-    if (P != p->tab_P || vec != p->tab_vec || ldp > p->tab_L.ldp) {
+    if (P != p->tab_P || vec != p->tab_vec || (sw > 0) != p->tab_sliced || ldp > p->tab_L.ldp) {
       const hipError_t eb = build_device_tables(p, N, vec, s);
       if (eb != hipSuccess) return eb == hipErrorOutOfMemory ? CSRSPMM_STATUS_ALLOC_FAILED : (int)eb;
     }
     bind_tables(p, pr, vec);
     pr.plan_ready = true;
     pr.dp_ready = true;
-    pr.sw = P > 0 ? 0
-                  : slice_width(p->K, N, false,
-                                wide_sweep(vec, true, p->M, p->K, p->nnz));
+    pr.sw = sw;
     pr.slice_launch = slice_launches(p->M, p->nnz);
     return to_status(launch_algorithm(p->algo, pr, s));
   }

@@ -104,10 +104,14 @@ __device__ __forceinline__ int clamp_nnz(int x, int nnz) { return min(max(x, 0),
 // row * ldb * 4 + column * 4 is one 32-bit v_mad_u32_u24 instead of 64-bit
 // address arithmetic, and the hardware range-checks it against B's extent (an
 // offset at or past the end reads 0 and fetches nothing).  The host picks BUF
-// only when B's extent is at most kBufMaxBytes and rows and row lengths fit
-// 24 bits (buf_gathers_ok), so a valid offset stays below kBufOffPast and an
-// offset of kBufOffPast or more, plus any column byte offset, still lies past
-// the end without wrapping.
+// only when B's extent is below kBufOffPast and rows and row lengths fit 24
+// bits (buf_gathers_ok), so a valid offset stays below kBufOffPast, and an
+// entry past a chunk's count (offset kBufOffPast plus a column byte offset)
+// lies past the end without wrapping.  A lane whose column lies past the
+// block's columns adds kBufOffPast to a valid row offset, which stays past
+// the end only while the row offset is below 2^32 - kBufOffPast (1 GiB):
+// buf_gathers_ok allows a larger B only when no lane's column can be past
+// the end.
 constexpr unsigned kBufOffPast = 0xC0000000u;
 struct BufB {
   __amdgpu_buffer_rsrc_t rsrc;
@@ -186,9 +190,10 @@ __device__ __forceinline__ void chunk_gather(const Problem& p, const Panel<VEC, 
     }
   };
   if constexpr (BUF) {
-    // Full batches of U need no per-entry masks; the last, partial batch
-    // gives its missing entries an offset past the buffer and skips them.
-    // k is a multiple of U below cnt <= G, so k + u < G.
+    // Full batches of U need no per-entry masks (k + u < cnt <= G); the
+    // last, partial batch gives its missing entries an offset past the
+    // buffer and skips them, and reads their (col, val) from within the
+    // group (index masked: U may exceed G, as in the scalar 4-lane kernels).
     int k = 0;
     for (; k + U <= cnt; k += U) {
       int c[U];
@@ -209,7 +214,7 @@ __device__ __forceinline__ void chunk_gather(const Problem& p, const Panel<VEC, 
       int c[U];
       float v[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) pair(k + u, c[u], v[u]);
+      for (int u = 0; u < U; ++u) pair((k + u) & (G - 1), c[u], v[u]);
       VT b[U][T];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -1508,12 +1513,18 @@ static hipError_t dispatch_vec4_cols(const Problem& p, hipStream_t s) {
 }
 
 // B can be gathered through a buffer resource: every row and row length fits
-// 24 bits (one v_mad_u32_u24 per offset) and B's extent stays below
-// kBufOffPast.
-static bool buf_gathers_ok(const Problem& p) {
+// 24 bits (one v_mad_u32_u24 per offset), B's extent stays below
+// kBufOffPast, and either it stays within 1 GiB or no lane of any group owns
+// a column past the block's columns (a power of two of at least 4 vec
+// columns per block, which the column slices divide): a masked lane's
+// offset, row offset + kBufOffPast, then cannot wrap into the buffer.
+static bool buf_gathers_ok(const Problem& p, int vec) {
   if (p.K <= 0 || p.K >= (1 << 24) || p.ldb * 4 >= (1LL << 24)) return false;
   const long long bytes = (long long)(p.K - 1) * p.ldb * 4 + (long long)p.N * 4;
-  return bytes < (long long)kBufOffPast;
+  if (bytes >= (long long)kBufOffPast) return false;
+  if (bytes <= (1LL << 30)) return true;
+  const int cols = p.sw > 0 ? p.sw : p.N;
+  return (cols & (cols - 1)) == 0 && cols >= 4 * vec && (p.sw == 0 || p.N % p.sw == 0);
 }
 
 // The kernel shape comes from the columns one block covers: a column slice,
@@ -1542,15 +1553,15 @@ static hipError_t dispatch_vec4(const Problem& p, hipStream_t s) {
   if (p.sw == kSliceWidth) {
     // The short rows of each slice are swept band by band (sweep_rows); the
     // LDS-staged variant passes each chunk through its stage.
-    if (sweep_applies(p.plan, p.M, p.K, p.nnz, p.sw) && buf_gathers_ok(p)) {
+    if (sweep_applies(p.plan, p.M, p.K, p.nnz, p.sw) && buf_gathers_ok(p, 4)) {
       Problem q = p;
       sweep_geometry(p.K, p.sw, q.sweep_shift, q.sweep_bands);
       return launch_rg<4, 16, 1, kVec4U, LDS, CSRSPMM_SWEEP_SU, true, true>(q, s);
     }
-    if (buf_gathers_ok(p)) return launch_rg<4, 16, 1, kVec4U, LDS, 8, true>(p, s);
+    if (buf_gathers_ok(p, 4)) return launch_rg<4, 16, 1, kVec4U, LDS, 8, true>(p, s);
     return launch_rg<4, 16, 1, kVec4U, LDS, 8>(p, s);
   }
-  if (buf_gathers_ok(p)) return dispatch_vec4_cols<LDS, true>(p, s);
+  if (buf_gathers_ok(p, 4)) return dispatch_vec4_cols<LDS, true>(p, s);
   return dispatch_vec4_cols<LDS, false>(p, s);
 }
 
@@ -1583,7 +1594,7 @@ static hipError_t dispatch_vec1_cols(const Problem& p, hipStream_t s) {
 // R-MAT N = 64 (Auto) within 0.6%.
 template <bool LDS>
 static hipError_t dispatch_vec1(const Problem& p, hipStream_t s) {
-  if (buf_gathers_ok(p)) return dispatch_vec1_cols<LDS, true>(p, s);
+  if (buf_gathers_ok(p, 1)) return dispatch_vec1_cols<LDS, true>(p, s);
   return dispatch_vec1_cols<LDS, false>(p, s);
 }
 

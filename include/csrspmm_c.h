@@ -241,11 +241,15 @@ int csrspmm_spmm_f32_ex(int algo, int M, int K, int N, int nnz,
  * forbid hipMalloc).  The workspace is a static device array of
  * CSRSPMM_NOALLOC_SCRATCH_BYTES (128 MiB) in the library, one per GPU, which
  * each GPU the library runs on holds until the process ends.  A problem whose
- * base workspace, csrspmm_workspace_bytes(algo, M, N, nnz), exceeds it is
- * rejected with CSRSPMM_STATUS_SCRATCH_TOO_SMALL before anything is
- * enqueued; one whose per-call column-panel tables do not fit as well runs
- * without panels (the same result, more slowly).  The five benchmark
- * configurations all fit, with their panels.  Calls no hipMalloc or hipFree
+ * base workspace (block starts, segment slots and partials of the call's own
+ * plan; none when the call runs as one launch, as a max_row_nnz hint can
+ * make it) exceeds it is rejected with CSRSPMM_STATUS_SCRATCH_TOO_SMALL
+ * before anything is enqueued; one whose per-call column-panel or XCD share
+ * tables do not fit as well runs without them (more slowly; without the
+ * shares, rows above 128 nonzeros are summed in CSR order segment by
+ * segment, a result within the same bound).  The five benchmark
+ * configurations all fit, with their panels (R-MAT without its shares).
+ * Calls no hipMalloc or hipFree
  * (the first call on a device looks the array's address up once).
  * All calls on one GPU share its array: calls that overlap on one GPU (on
  * different streams, or from different threads) race and give wrong

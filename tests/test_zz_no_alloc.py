@@ -96,3 +96,26 @@ def test_noalloc_rejects_beyond_scratch(gpu):
     assert "no-allocation scratch" in str(e.value)
     torch.cuda.synchronize()
     assert bool((C == 7.0).all())
+
+
+def test_noalloc_hinted_one_launch(gpu):
+    """A max_row_nnz hint that makes a mid-sized call one launch (rows of at
+    most 256, M < 32768, no column slices) needs no workspace, even where
+    the unhinted plan's partials would exceed the scratch (rows of 200 on
+    1024 x 256 with N = 16384: segments of 32, 419 MB of partials): the call
+    runs, bit for bit as _ex, within the bar of the oracle, twice in a row."""
+    M, K, N = 1024, 256, 16384
+    a = gen.uniform(M, K, 200, 23)
+    lib = capi.hip()
+    assert lib.csrspmm_workspace_bytes(capi.ALGO["Auto"], M, N, a.nnz) > 128 << 20
+    assert lib.csrspmm_workspace_bytes_ex(capi.ALGO["Auto"], M, K, N, a.nnz, 200) == 0
+    B = gen.dense(23, gen.TAG_B, K, N)
+    d = upload(gpu, a, B)
+    C0 = torch.zeros((M, N), device=gpu)
+    rows = np.arange(0, M, 16).astype(np.int32)
+    R, S = oracle.spmm_f64(a.rowptr, a.colidx, a.vals, B, None, 1.0, 0.0, rows=rows)
+    for _ in range(2):
+        C_na, C_ex = run_pair("Auto", a, B, d, C0, 1.0, 0.0, hint=200)
+        assert torch.equal(C_na, C_ex)
+        bad, ratio, _, _ = oracle.check(C_na.cpu().numpy()[rows], R, S, 1e-5)
+        assert bad == 0, f"max ratio {ratio}"
