@@ -23,6 +23,9 @@ stream.  Prints ONE JSON line:
              reference's spmm() pays) and cold (after a 512 MiB scratch write
              that flushes L2 and the MALL)
   variants   the same figures for every variant on the same config
+  configs    per-variant ms, GFLOPS and (where profiles/traffic.json holds
+             the key) measured HBM fraction of Auto and every variant on the
+             other BASELINE configs (medium, large, rmat, rmat512 by default)
   plan       the same figures for a stored plan (csrspmm_plan_*, Auto by
              default) built once outside the timed region, with its build
              time; the headline stays the per-call path, which needs no
@@ -59,6 +62,8 @@ def parse():
     ap.add_argument("--algo", default="Auto")
     ap.add_argument("--variants", default="all", help="'all', 'none' or comma list")
     ap.add_argument("--variant-steps", type=int, default=20)
+    ap.add_argument("--configs", default="medium,large,rmat,rmat512",
+                    help="per-config leg: comma list of other configs ('none' disables it)")
     ap.add_argument("--plan-algo", default="Auto", help="stored-plan leg ('none' disables it)")
     ap.add_argument("--mode-calls", type=int, default=30,
                     help="calls per timing mode (warm / api / cold) of the headline variant")
@@ -66,6 +71,71 @@ def parse():
                     help="time budget of the CPU baseline leg (0 disables it)")
     ap.add_argument("--traffic-file", default=os.path.join(HERE, "profiles", "traffic.json"))
     return ap.parse_args()
+
+
+def load_config(capi, torch, cfg, dev, algos):
+    """(csr, B on the host, device inputs + a workspace for every algo)."""
+    a = cfg.csr()
+    B = cfg.B(a.K)
+    N = cfg.N
+    d = {
+        "rowptr": torch.from_numpy(a.rowptr).to(dev),
+        "colidx": torch.from_numpy(a.colidx).to(dev),
+        "vals": torch.from_numpy(a.vals).to(dev),
+        "B": torch.from_numpy(B).to(dev),
+        "C": torch.empty((a.M, N), dtype=torch.float32, device=dev),
+    }
+    need = max(capi.hip().csrspmm_workspace_bytes_ex(capi.ALGO[x], a.M, a.K, N, a.nnz, -1)
+               for x in algos)
+    d["ws"] = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
+    torch.cuda.synchronize()
+    return a, B, d
+
+
+def figures(cfg, a, ms, main_ms, traffic_file, key=None, bmin=None, balg=None):
+    """GFLOPS and HBM fractions of one timed variant on one config."""
+    from csrspmm_amd import configs
+
+    flops = configs.flops(a.nnz, cfg.N)
+    f = {
+        "ms": round(ms, 5),
+        "main_kernel_ms": round(main_ms, 5),
+        "gflops": round(flops / (ms * 1e-3) / 1e9, 2),
+    }
+    if bmin is not None:
+        f["compulsory_frac"] = round(bmin / (main_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+    if balg is not None:
+        f["gather_model_gbs"] = round(balg / (main_ms * 1e-3) / 1e9, 1)
+    if key is not None:
+        e, fresh = traffic_entry(traffic_file, key)
+        if e is not None:
+            gbs = e["bytes_per_call"] / (main_ms * 1e-3) / 1e9
+            f["measured_gbs"] = round(gbs, 1)
+            f["measured_frac"] = round(gbs / HBM_PEAK_GBS, 4)
+            f["traffic_current"] = fresh
+    return f
+
+
+def config_leg(capi, torch, name, dev, args):
+    """Auto and every variant on one more config: {algo: figures}."""
+    from csrspmm_amd import ALGORITHMS, configs
+
+    cfg = configs.CONFIGS[name]
+    t0 = time.perf_counter()
+    a, _, d = load_config(capi, torch, cfg, dev, ALGORITHMS)
+    lib = capi.hip()
+    resolved = lib.csrspmm_algorithm_name(
+        lib.csrspmm_resolve_algorithm_ex(capi.ALGO["Auto"], a.M, a.K, cfg.N, a.nnz, -1)).decode()
+    out = {"M": a.M, "K": a.K, "N": cfg.N, "nnz": a.nnz, "resolved_auto": resolved, "algos": {}}
+    for algo in ("Auto",) + tuple(ALGORITHMS):
+        ms, main_ms = time_variant(capi, torch, algo, d, args.variant_steps, 3)
+        out["algos"][algo] = figures(cfg, a, ms, main_ms, args.traffic_file, f"{name}/{algo}")
+    del d
+    torch.cuda.empty_cache()
+    out["seconds"] = round(time.perf_counter() - t0, 1)
+    print(f"[bench] config {name}: Auto ({resolved}) {out['algos']['Auto']['ms']:.4f} ms/call, "
+          f"leg {out['seconds']} s", file=sys.stderr, flush=True)
+    return out
 
 
 def time_variant(capi, torch, algo, d, steps, warmup):
@@ -264,45 +334,19 @@ def main():
     dev = torch.device("cuda:0")
     cfg = configs.CONFIGS[args.config]
     t0 = time.perf_counter()
-    a = cfg.csr()
-    B = cfg.B(a.K)
+    a, B, d = load_config(capi, torch, cfg, dev, ALGORITHMS)
     gen_s = time.perf_counter() - t0
     print(f"[bench] {cfg.name}: M={a.M} nnz={a.nnz} N={cfg.N} max_row={a.max_row_nnz} "
-          f"(generated in {gen_s:.1f}s)", file=sys.stderr, flush=True)
+          f"(generated and uploaded in {gen_s:.1f}s)", file=sys.stderr, flush=True)
     N = cfg.N
-    d = {
-        "rowptr": torch.from_numpy(a.rowptr).to(dev),
-        "colidx": torch.from_numpy(a.colidx).to(dev),
-        "vals": torch.from_numpy(a.vals).to(dev),
-        "B": torch.from_numpy(B).to(dev),
-        "C": torch.empty((a.M, N), dtype=torch.float32, device=dev),
-    }
-    need = max(capi.hip().csrspmm_workspace_bytes_ex(capi.ALGO[x], a.M, a.K, N, a.nnz, -1)
-               for x in ALGORITHMS)
-    d["ws"] = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
-    torch.cuda.synchronize()
 
     flops = configs.flops(a.nnz, N)
     balg = configs.bytes_alg(a.M, a.nnz, N, False)
     U = configs.distinct_columns(a.colidx, a.K)
     bmin = configs.bytes_min(a.M, a.nnz, N, U, False)
 
-    def figures(ms, main_ms, key=None):
-        f = {
-            "ms": round(ms, 5),
-            "main_kernel_ms": round(main_ms, 5),
-            "gflops": round(flops / (ms * 1e-3) / 1e9, 2),
-            "compulsory_frac": round(bmin / (main_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "gather_model_gbs": round(balg / (main_ms * 1e-3) / 1e9, 1),
-        }
-        if key is not None:
-            e, fresh = traffic_entry(args.traffic_file, key)
-            if e is not None:
-                gbs = e["bytes_per_call"] / (main_ms * 1e-3) / 1e9
-                f["measured_gbs"] = round(gbs, 1)
-                f["measured_frac"] = round(gbs / HBM_PEAK_GBS, 4)
-                f["traffic_current"] = fresh
-        return f
+    def fig(ms, main_ms, key=None):
+        return figures(cfg, a, ms, main_ms, args.traffic_file, key, bmin, balg)
 
     lib = capi.hip()
     resolved = lib.csrspmm_algorithm_name(
@@ -316,10 +360,10 @@ def main():
         names = ALGORITHMS if args.variants == "all" else args.variants.split(",")
         for name in names:
             if name == resolved:
-                variants[name] = figures(ms, main_ms, f"{cfg.name}/{args.algo}")
+                variants[name] = fig(ms, main_ms, f"{cfg.name}/{args.algo}")
                 continue
             vms, vmain = time_variant(capi, torch, name, d, args.variant_steps, 3)
-            variants[name] = figures(vms, vmain, f"{cfg.name}/{name}")
+            variants[name] = fig(vms, vmain, f"{cfg.name}/{name}")
             print(f"[bench] {name}: {vms:.4f} ms/call", file=sys.stderr, flush=True)
 
     modes = None
@@ -332,12 +376,20 @@ def main():
         plan, build_ms, pms, pmain = time_plan(capi, torch, args.plan_algo, d, a.K, N,
                                                args.variant_steps, 3)
         plan_fig = {"algo": args.plan_algo, "resolved": plan.algorithm,
-                    **figures(pms, pmain, f"{cfg.name}/plan{args.plan_algo}"),
+                    **fig(pms, pmain, f"{cfg.name}/plan{args.plan_algo}"),
                     "build_ms": round(build_ms, 2), "device_bytes": plan.device_bytes,
                     "panelized_rows": plan.panelized_rows}
         plan.close()
         print(f"[bench] plan {plan_fig['resolved']}: {pms:.4f} ms/call, main {pmain:.4f} ms, "
               f"built in {build_ms:.1f} ms", file=sys.stderr, flush=True)
+
+    per_config = {}
+    if args.configs != "none":
+        del d  # the headline config's device inputs
+        torch.cuda.empty_cache()
+        for name in args.configs.split(","):
+            if name and name != cfg.name:
+                per_config[name] = config_leg(capi, torch, name, dev, args)
 
     from csrspmm_amd import kernel_source_digest
 
@@ -393,6 +445,7 @@ def main():
         "modes": modes,
         "variants": variants,
         "plan": plan_fig,
+        "configs": per_config,
     }
     print(json.dumps(out), flush=True)
 

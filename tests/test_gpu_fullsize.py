@@ -1,6 +1,6 @@
-"""Full-size checks that need no fp64 oracle over the whole output (which
-would take minutes at these sizes); the sampled-row oracle tests in
-test_gpu_parity.py cover the values themselves.
+"""Full-size checks that need no oracle: identities and closed forms over
+the whole output, for every variant and config path (test_gpu_parity.py
+holds the every-element fp64 oracle comparison of the BASELINE configs).
 
 * Exact identities, bit for bit over every element of C: B scaled by 2 gives
   2 C (every product and partial sum scales by a power of two, exactly);
@@ -16,8 +16,8 @@ test_gpu_parity.py cover the values themselves.
   |colsum error| <= 1e-5 * sum_k |w|[k] |B[k, j]| (|w| from |values|), so
   every row of the full matrix takes part: a row or a long segment dropped
   or counted twice anywhere shows (a dropped 400-nonzero row measured 27x
-  the bound on a small case), where the sampled rows might miss it.  Small
-  value errors are left to the sampled oracle rows and the identities.
+  the bound on a small case).  Small value errors are left to the oracle
+  comparison and the identities.
 """
 import functools
 

@@ -12,9 +12,10 @@ the same order; longer rows are split into near-equal segments whose partial
 sums are added in a fixed order, which is within the tolerance but not
 bitwise.
 
-The full-size configs are checked on a row sample (every row for host and
-medium; 4096 random rows plus the 64 longest and some empty rows otherwise)
-so the oracle finishes in seconds.
+Every BASELINE config is checked on every element of C, for Auto and each
+variant: the fp64 oracle and the fp32 restatement are OpenMP loops over rows
+(R-MAT at N = 64, 16 M nonzeros: about 0.6 s on 8 cores), computed once per
+config and shared by its variants.
 """
 import functools
 
@@ -57,13 +58,17 @@ def run_spmm(algo, rowptr, colidx, vals, B, dev, C0=None, alpha=1.0, beta=0.0, h
 
 
 def assert_parity(algo, C, rowptr, colidx, vals, B, C0, alpha, beta, rows=None, c0_zero=False,
-                  what="", hint=-1, shares=None):
-    R, S = oracle.spmm_f64(rowptr, colidx, vals, B, C0, alpha, beta, c0_zero=c0_zero, rows=rows)
+                  what="", hint=-1, shares=None, ref=None):
+    """ref: (R, S, F) of these inputs, already computed, or None."""
+    if ref is None:
+        R, S = oracle.spmm_f64(rowptr, colidx, vals, B, C0, alpha, beta, c0_zero=c0_zero, rows=rows)
+        F = oracle.spmm_f32_seq(rowptr, colidx, vals, B, C0, alpha, beta, c0_zero=c0_zero, rows=rows)
+    else:
+        R, S, F = ref
     Cs = C if rows is None else C[rows]
     bad, ratio, plain, worst = oracle.check(Cs, R, S, TOL)
     assert bad == 0, f"{algo} {what}: {bad} elements out of tolerance (max ratio {ratio:.3g})"
     # bitwise against the fp32 restatement on rows summed whole
-    F = oracle.spmm_f32_seq(rowptr, colidx, vals, B, C0, alpha, beta, c0_zero=c0_zero, rows=rows)
     ridx = np.arange(rowptr.size - 1) if rows is None else np.asarray(rows)
     lens = rowptr[ridx + 1] - rowptr[ridx]
     whole = (np.ones_like(lens, dtype=bool) if algo in WHOLE_ROW_ALGOS
@@ -102,6 +107,16 @@ def config_data(name):
     return cfg, a, B
 
 
+@functools.lru_cache(maxsize=1)
+def config_ref(name):
+    """(R, S, F) over every row of a config (one config held at a time: the
+    tests below run config by config)."""
+    cfg, a, B = config_data(name)
+    R, S = oracle.spmm_f64(a.rowptr, a.colidx, a.vals, B)
+    F = oracle.spmm_f32_seq(a.rowptr, a.colidx, a.vals, B)
+    return R, S, F
+
+
 def sample_rows(a, full):
     if full:
         return None
@@ -113,15 +128,18 @@ def sample_rows(a, full):
     return np.unique(np.concatenate([longest, empty, rnd])).astype(np.int32)
 
 
-@pytest.mark.parametrize("algo", ALGORITHMS)
-@pytest.mark.parametrize("cfg_name", ["host", "medium", "large", "xl", "rmat", "rmat512", "xl98"])
+# algo varies fastest, so each config's oracle is computed once
+@pytest.mark.parametrize("algo", ("Auto",) + ALGORITHMS)
+@pytest.mark.parametrize("cfg_name", ["host", "medium", "large", "xl", "xl98", "rmat", "rmat512"])
 def test_config(cfg_name, algo, gpu):
+    """Every element of C against the fp64 oracle (and, on rows summed
+    whole, the fp32 restatement bit for bit)."""
     cfg, a, B = config_data(cfg_name)
-    print(f"[parity] {cfg_name} {algo} M={a.M} nnz={a.nnz} N={cfg.N}", flush=True)
+    print(f"[parity] {cfg_name} {algo} M={a.M} nnz={a.nnz} N={cfg.N} (every row)", flush=True)
     C = run_spmm(algo, a.rowptr, a.colidx, a.vals, B, gpu, alpha=1.0, beta=0.0)
     assert not np.isnan(C).any(), "unwritten output elements"
-    rows = sample_rows(a, cfg_name in ("host", "medium"))
-    assert_parity(algo, C, a.rowptr, a.colidx, a.vals, B, None, 1.0, 0.0, rows=rows, what=cfg_name)
+    assert_parity(algo, C, a.rowptr, a.colidx, a.vals, B, None, 1.0, 0.0, what=cfg_name,
+                  ref=config_ref(cfg_name))
 
 
 def test_xl_deterministic_and_hint_independent(gpu):
