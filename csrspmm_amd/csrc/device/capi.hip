@@ -37,6 +37,8 @@ WorkspaceLayout workspace_layout(int M, int K, int N, int nnz, int P, bool share
   off = align256(off + (size_t)L.nslots * sizeof(int2));
   L.partials_off = off;
   off = align256(off + (size_t)(nnz >> g.seg_shift) * (size_t)L.ldp * sizeof(float));
+  L.need_off = off;
+  off = align256(off + (size_t)plan_row_blocks(M));
   L.base_total = off;
   if (P > 0 && K > 0) {
     const long long w = ((long long)K + P - 1) / P;
@@ -82,6 +84,8 @@ void bind_workspace(Problem& p, void* ws, const WorkspaceLayout& L, int mblk) {
   p.block_start = reinterpret_cast<int*>(b + L.block_start_off);
   p.seg_info = reinterpret_cast<int2*>(b + L.seg_info_off);
   p.partials = reinterpret_cast<float*>(b + L.partials_off);
+  p.need = reinterpret_cast<unsigned char*>(b + L.need_off);
+  p.need_blocks = plan_row_blocks(p.M);
   p.ldp = L.ldp;
   p.nslots = L.nslots;
   p.mblk = mblk;
@@ -511,6 +515,11 @@ int spmm_impl(int algo_in, int M, int K, int N, int nnz, const int* rowptr, cons
     int P = per_call_panels(vec, true, K, N, nnz, hint);
     p.sw = slice_width(K, N, P > 0, wide_sweep(vec, true, M, K, nnz));
     p.slice_launch = slice_launches(M, nnz);
+    if (p.sw == 0 && P == 0 && vec == 4 && xcd_slices(K, N) > 0) {
+      p.sw = kSliceWidth;
+      p.slice_launch = false;
+      p.xslice = true;
+    }
     if (p.sw > 0) P = 0;  // a sliced call gathers band by band instead
     WorkspaceLayout L = workspace_layout(M, K, N, nnz, P, share_applies(true, K, N, nnz, p.sw, P, hint));
     if (owned) {
@@ -527,7 +536,8 @@ int spmm_impl(int algo_in, int M, int K, int N, int nnz, const int* rowptr, cons
       // a workspace sized without the panel or share tables runs without them
       if (ws_bytes < L.total) L = workspace_layout(M, K, N, nnz, 0);
     }
-    bind_workspace(p, ws, L, call_merge_block(vec, M, nnz, p.sw > 0));
+    // XCD slices keep the unsliced merge blocks (each launch holds every slice)
+    bind_workspace(p, ws, L, call_merge_block(vec, M, nnz, p.sw > 0 && !p.xslice));
     set_row_hint(p, hint);
   }
   return to_status(launch_algorithm(algo, p, s));

@@ -331,9 +331,12 @@ int device_panels(const csrspmm_plan_s* p, int vec, int N) {
   return slice_width(p->K, N, P > 0) > 0 ? 0 : P;
 }
 
-// Column-slice width of a call of N with P panels: the per-call rule.
-int device_slice_width(const csrspmm_plan_s* p, int vec, int N, int P) {
-  return P > 0 ? 0 : slice_width(p->K, N, false, wide_sweep(vec, true, p->M, p->K, p->nnz));
+// Column slices of a call of N with P panels (npan panelized rows): the
+// per-call rules, column slices or else XCD slices.
+void call_slicing(const csrspmm_plan_s* p, int vec, int N, int P, int& sw, bool& xslice) {
+  sw = P > 0 ? 0 : slice_width(p->K, N, false, wide_sweep(vec, true, p->M, p->K, p->nnz));
+  xslice = sw == 0 && P == 0 && vec == 4 && xcd_slices(p->K, N) > 0;
+  if (xslice) sw = kSliceWidth;
 }
 
 // A Problem carrying the plan's CSR and tables (B and C are the call's); the
@@ -367,7 +370,10 @@ hipError_t build_device_tables(csrspmm_plan_s* p, int N, int vec, hipStream_t s)
   p->tab_n = N;
   p->tab_vec = vec;
   p->tab_P = P;
-  p->tab_sliced = device_slice_width(p, vec, N, P) > 0;
+  int sw;
+  bool xslice;
+  call_slicing(p, vec, N, P, sw, xslice);
+  p->tab_sliced = sw > 0 && !xslice;  // XCD slices keep the unsliced merge blocks
   Problem q{};
   q.M = p->M;
   q.K = p->K;
@@ -476,9 +482,12 @@ int csrspmm_plan_spmm_f32(csrspmm_plan_t plan, int N, const float* B, long long 
     // panels, column width or partial width differ from theirs
     const int vec = vector_width(p->algo, pr);
     const int P = device_panels(p, vec, N);
-    const int sw = device_slice_width(p, vec, N, P);
+    int sw;
+    bool xslice;
+    call_slicing(p, vec, N, P, sw, xslice);
     const long long ldp = ((long long)N + 3) & ~3LL;
-    if (P != p->tab_P || vec != p->tab_vec || (sw > 0) != p->tab_sliced || ldp > p->tab_L.ldp) {
+    if (P != p->tab_P || vec != p->tab_vec || (sw > 0 && !xslice) != p->tab_sliced ||
+        ldp > p->tab_L.ldp) {
       const hipError_t eb = build_device_tables(p, N, vec, s);
       if (eb != hipSuccess) return eb == hipErrorOutOfMemory ? CSRSPMM_STATUS_ALLOC_FAILED : (int)eb;
     }
@@ -486,7 +495,8 @@ int csrspmm_plan_spmm_f32(csrspmm_plan_t plan, int N, const float* B, long long 
     pr.plan_ready = true;
     pr.dp_ready = true;
     pr.sw = sw;
-    pr.slice_launch = slice_launches(p->M, p->nnz);
+    pr.slice_launch = !xslice && slice_launches(p->M, p->nnz);
+    pr.xslice = xslice;
     return to_status(launch_algorithm(p->algo, pr, s));
   }
   hipError_t e = ensure_partials(p, N, s);
@@ -504,10 +514,12 @@ int csrspmm_plan_spmm_f32(csrspmm_plan_t plan, int N, const float* B, long long 
   pr.npan = p->npan;
   const int vec = vector_width(p->algo, pr);
   const bool lds = uses_lds(p->algo);
-  // a plan with panelized rows keeps them; otherwise large B are sliced by columns
-  pr.sw = p->npan > 0 ? 0
-                      : slice_width(p->K, N, false, wide_sweep(vec, true, p->M, p->K, p->nnz));
-  pr.slice_launch = slice_launches(p->M, p->nnz);
+  // a plan with panelized rows keeps them; otherwise large B are sliced by
+  // columns (or by XCD)
+  bool xslice;
+  call_slicing(p, vec, N, p->npan, pr.sw, xslice);
+  pr.slice_launch = !xslice && slice_launches(p->M, p->nnz);
+  pr.xslice = xslice;
   pr.pan_rows = p->d_pan_rows;
   pr.pan_ptr = p->d_pan_ptr;
   pr.pan_piece = p->d_pan_piece;

@@ -759,8 +759,15 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(SWE
   // launch holds one slice or all of them in slice order (launch_rg).
   int c_lo = 0, c_hi = p.N;
   if (p.sw > 0) {
-    const int local = bid / slice_blocks;  // bid counts from this launch's first slice, slice0
-    bid -= local * slice_blocks;            // now in [0, slice_blocks)
+    int local;
+    if (p.xslice) {  // all slices in this launch, interleaved block by block
+      const int ns = (p.N + p.sw - 1) / p.sw;
+      local = bid % ns;
+      bid /= ns;
+    } else {
+      local = bid / slice_blocks;  // bid counts from this launch's first slice, slice0
+      bid -= local * slice_blocks;  // now in [0, slice_blocks)
+    }
     c_lo = (slice0 + local) * p.sw;
     c_hi = min(p.N, c_lo + p.sw);
   }
@@ -897,6 +904,7 @@ __global__ __launch_bounds__(256) void plan_kernel(Problem p) {
   const int lane = lane_id();
   if (p.dp.P > 0 && rblock == 0)
     for (int q = (int)threadIdx.x; q < p.dp.P; q += blockDim.x) p.dp.sched[kPanelHist + q] = 0;
+  int need = 0;  // a row of this block needs the combine
   // block-uniform trip count, so every wave reaches the ballot below whole
   for (int base = rblock * blockDim.x; base <= p.M; base += stride) {
     const int r = base + (int)threadIdx.x;
@@ -916,6 +924,7 @@ __global__ __launch_bounds__(256) void plan_kernel(Problem p) {
         s0 = x0 >> p.slot_shift;
         s1 = min(max(s0, x1 >> p.slot_shift), p.nslots);
         nseg = seg_count(p, x1 - x0);
+        need |= nseg >= 2 || (p.shares && nseg >= 1) || (p.dp.P > 0 && x1 - x0 >= kPanelMinLen);
         if (p.dp.P > 0) {
           // windows w whose first position w * kPanelMinLen lies in this row
           w0 = (x0 + kPanelMinLen - 1) / kPanelMinLen;
@@ -937,6 +946,8 @@ __global__ __launch_bounds__(256) void plan_kernel(Problem p) {
                        __builtin_amdgcn_readlane(x0, l), __builtin_amdgcn_readlane(x1, l), lane, 64);
     }
   }
+  need = __syncthreads_or(need);
+  if (p.need && threadIdx.x == 0 && rblock < p.need_blocks) p.need[rblock] = (unsigned char)(need != 0);
 }
 
 // XCD shares (Problem::shares).  The first slot s of a split row (fewer
@@ -1266,6 +1277,26 @@ __device__ __forceinline__ void store_cols4(const Problem& p, float* cptr, int c
 // kScanSlots / 2 rows to sum (with XCD shares, kScanSlots rows).
 constexpr int kScanSlots = 16;
 
+// Whether any row block of plan_kernel flagged a row for the combine (every
+// wave reads the flags, 16 a load, and all reach the same answer).
+__device__ __forceinline__ bool combine_needed(const Problem& p, int lane) {
+  if (!p.need) return true;
+  const uint4* f4 = reinterpret_cast<const uint4*>(p.need);
+  bool any = false;
+  for (int i = lane; i * 16 < p.need_blocks; i += 64) {
+    const uint4 x = f4[i];
+    const int valid = min(p.need_blocks - i * 16, 16);  // bytes past need_blocks are padding
+    const unsigned w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int nb = min(max(valid - 4 * j, 0), 4);
+      const unsigned m = nb >= 4 ? 0xffffffffu : (1u << (8 * nb)) - 1u;
+      any |= (w[j] & m) != 0;
+    }
+  }
+  return __ballot(any) != 0;
+}
+
 template <int VEC, int GC>
 __global__ __launch_bounds__(kWaves * 64) void combine_kernel(Problem p, int scan_blocks) {
   constexpr int P = 64 / GC;
@@ -1273,6 +1304,7 @@ __global__ __launch_bounds__(kWaves * 64) void combine_kernel(Problem p, int sca
   const int q = lane / GC;
   const int gl = lane & (GC - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (!combine_needed(p, lane)) return;  // no split, shared or panelized row
   if ((int)blockIdx.x < scan_blocks) {
     const int nchunks = div_up(p.nslots, kScanSlots);
     for (int ch = blockIdx.x * kWaves + wave; ch < nchunks; ch += scan_blocks * kWaves) {
@@ -1475,7 +1507,7 @@ static inline int pow2_ceil(int x) {
 template <bool LDS, bool BUF>
 static hipError_t dispatch_vec4_cols(const Problem& p, hipStream_t s) {
   constexpr int SU = CSRSPMM_SEG_UNROLL;
-  const int nv = p.N / 4;
+  const int nv = (p.sw > 0 ? std::min(p.sw, p.N) : p.N) / 4;
   const int G = nv >= 64 ? 64 : (pow2_ceil(nv) < 4 ? 4 : pow2_ceil(nv));
   if constexpr (BUF) {
     const long long mean4 = p.M > 0 ? 4LL * p.nnz / p.M : 0;
@@ -1601,7 +1633,7 @@ static hipError_t dispatch_vec1(const Problem& p, hipStream_t s) {
 // plan_kernel's grid: blocks of 256 rows (grid-strided beyond 4096), and
 // with XCD shares one more block for their column boundaries.
 static int plan_blocks(const Problem& p) {
-  return std::min(div_up_host(p.M + 1, 256), 4096) + (p.shares ? 1 : 0);
+  return plan_row_blocks(p.M) + (p.shares ? 1 : 0);
 }
 
 hipError_t launch_share_bounds(const Problem& p, hipStream_t s) {

@@ -291,6 +291,30 @@ inline int slice_width(int K, int N, bool panels, bool sweeps = false) {
   return kSliceWidth;
 }
 
+// plan_kernel's row blocks: 256 rows each, grid-strided beyond kPlanMaxRowBlocks.
+constexpr int kPlanMaxRowBlocks = 4096;
+inline int plan_row_blocks(int M) {
+  const long long b = ((long long)M + 1 + 255) / 256;
+  return b < kPlanMaxRowBlocks ? (int)b : kPlanMaxRowBlocks;
+}
+
+// XCD slices (Problem::xslice): a float4 call whose B exceeds one XCD's L2
+// (kXcdL2Bytes) but whose kSliceWidth-column bands fit it runs 2, 4 or 8
+// slices in one launch, block b on slice b mod the slice count; blocks reach
+// the XCDs in turn (b mod kXcds), so each XCD gathers from one band only.
+// Measured on MI355X per call (rocprofv3), medium (16384^2, 82 per row,
+// N = 128, 8 MiB B): main kernel 45.5 -> 40.5 us; 4 slices of 32 columns
+// took 48.9 and 8 of 16 more (narrower gathers).  Returns the slice count
+// (0: none).
+constexpr long long kXcdL2Bytes = 4LL << 20;
+inline int xcd_slices(int K, int N) {
+  const long long full = (long long)K * N * 4;
+  const long long band = (long long)K * kSliceWidth * 4;
+  const int ns = (N + kSliceWidth - 1) / kSliceWidth;
+  if (ns < 2 || ns > kXcds || (ns & (ns - 1)) != 0) return 0;
+  return full > kXcdL2Bytes && band <= kXcdL2Bytes ? ns : 0;
+}
+
 // The plan is skipped for a hinted short-row problem (kPlanSkipItems).
 inline bool plan_skips(int M, int K, int N, int nnz, int hint) {
   return hint >= 0 && hint <= kPlanSkipMaxRow && M < kPlanSkipRows &&
@@ -378,6 +402,11 @@ struct Problem {
   int2* seg_info;     // per slot: (row, segment index) or (-1, 0) for an unused slot
   float* partials;    // nnz / seg partial rows of ldp floats
   long long ldp;
+  // Per row block of plan_kernel: 1 when a row of the block needs the
+  // combine (split into segments, by XCD or into panel pieces), else 0;
+  // written by plan_kernel on every call.  nullptr: the combine scans anyway.
+  unsigned char* need;
+  int need_blocks;
   // A stored plan (csrspmm_plan_create) filled block_start / seg_info once:
   // no plan_kernel launch per call.
   bool plan_ready;
@@ -398,6 +427,10 @@ struct Problem {
   // Slices as one launch each (true) or all in one launch, slice after slice
   // in block order (false).
   bool slice_launch;
+  // XCD slices (with slice_launch false): block b takes slice b mod the slice
+  // count instead, so a slice count dividing kXcds keeps each slice on the
+  // same XCDs and its band in their L2.
+  bool xslice;
   // From the caller's max_row_nnz hint (or a stored plan's true maximum):
   // rows_whole, no row above kLongRow: no segment phase (nslots = 0) and the
   // merge blocks sum every row whole, whatever its length, so a hint that is
@@ -551,7 +584,7 @@ inline void set_row_hint(Problem& p, int max_row_nnz) {
 // Workspace layout for a problem (all offsets 256-byte aligned).  P > 0 adds
 // the per-call panel tables and partial buffer after the base sections.
 struct WorkspaceLayout {
-  size_t block_start_off, seg_info_off, partials_off, base_total;
+  size_t block_start_off, seg_info_off, partials_off, need_off, base_total;
   size_t win_off, flag_off, pidx_off, list_off, bnd_off, sched_off, part_off, total;
   int nslots, nblocks;
   long long ldp;
