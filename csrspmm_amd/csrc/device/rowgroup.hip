@@ -775,6 +775,14 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(SWE
                                                      sweep_bnd);
 }
 
+// The combine checks the row blocks' flags (Problem::need) only without
+// column panels or XCD shares, which come with long rows: there the check
+// would only add its loads (XL: combine 10.6 -> 12.0 us, plan_kernel 6.3 ->
+// 6.9).
+__device__ __forceinline__ bool need_checked(const Problem& p) {
+  return p.need != nullptr && p.dp.P == 0 && !p.shares;
+}
+
 // Table entries of one row r: the merge-block starts [b_lo, b_hi], the
 // segment slots [s0, s1) (the first nseg hold segments) and the windows
 // [w0, w1), each range walked from `first` in steps of `step`.
@@ -946,8 +954,10 @@ __global__ __launch_bounds__(256) void plan_kernel(Problem p) {
                        __builtin_amdgcn_readlane(x0, l), __builtin_amdgcn_readlane(x1, l), lane, 64);
     }
   }
-  need = __syncthreads_or(need);
-  if (p.need && threadIdx.x == 0 && rblock < p.need_blocks) p.need[rblock] = (unsigned char)(need != 0);
+  if (need_checked(p)) {
+    need = __syncthreads_or(need);
+    if (threadIdx.x == 0 && rblock < p.need_blocks) p.need[rblock] = (unsigned char)(need != 0);
+  }
 }
 
 // XCD shares (Problem::shares).  The first slot s of a split row (fewer
@@ -1280,7 +1290,7 @@ constexpr int kScanSlots = 16;
 // Whether any row block of plan_kernel flagged a row for the combine (every
 // wave reads the flags, 16 a load, and all reach the same answer).
 __device__ __forceinline__ bool combine_needed(const Problem& p, int lane) {
-  if (!p.need) return true;
+  if (!need_checked(p)) return true;
   const uint4* f4 = reinterpret_cast<const uint4*>(p.need);
   bool any = false;
   for (int i = lane; i * 16 < p.need_blocks; i += 64) {
@@ -1470,7 +1480,7 @@ hipError_t launch_rg(const Problem& p, hipStream_t s) {
                          s, p, share_blocks, s0);
     }
     const long long blocks = (long long)piece_blocks + (long long)per_launch * slice_blocks;
-    if (blocks == 0) return hipSuccess;
+    if (blocks == 0) continue;
     if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
     if (piece_blocks > 0) {
       hipLaunchKernelGGL((rowgroup_kernel<VEC, G, T, U, LDS, kCanPanel, SU, BUF, false>), dim3((unsigned)blocks),
@@ -1649,6 +1659,11 @@ hipError_t launch_plan_tables(const Problem& p, hipStream_t s) {
   return hipGetLastError();
 }
 
+static hipError_t dispatch_main(const Problem& p, int vec, bool lds, hipStream_t s) {
+  if (vec == 4) return lds ? dispatch_vec4<true>(p, s) : dispatch_vec4<false>(p, s);
+  return lds ? dispatch_vec1<true>(p, s) : dispatch_vec1<false>(p, s);
+}
+
 static hipError_t launch_rowgroup_all(const Problem& p, int vec, bool lds, hipStream_t s) {
   if (p.plan && !p.plan_ready) hipLaunchKernelGGL(plan_kernel, dim3(plan_blocks(p)), dim3(256), 0, s, p);
   hipError_t e;
@@ -1661,11 +1676,7 @@ static hipError_t launch_rowgroup_all(const Problem& p, int vec, bool lds, hipSt
     e = launch_share_bounds(p, s);
     if (e != hipSuccess) return e;
   }
-  if (vec == 4) {
-    e = lds ? dispatch_vec4<true>(p, s) : dispatch_vec4<false>(p, s);
-  } else {
-    e = lds ? dispatch_vec1<true>(p, s) : dispatch_vec1<false>(p, s);
-  }
+  e = dispatch_main(p, vec, lds, s);
   if (e != hipSuccess) return e;
   if (p.plan && ((p.nslots > 0 && !p.no_split) || shares || p.npan > 0 || p.dp.P > 0)) {
     if (vec == 4) {
