@@ -1595,7 +1595,8 @@ static hipError_t dispatch_vec4(const Problem& p, hipStream_t s) {
   if (p.sw == kSliceWidth) {
     // The short rows of each slice are swept band by band (sweep_rows); the
     // LDS-staged variant passes each chunk through its stage.
-    if (sweep_applies(p.plan, p.M, p.K, p.nnz, p.sw) && buf_gathers_ok(p, 4)) {
+    // (XCD slices keep each band in one XCD's L2 without it.)
+    if (!p.xslice && sweep_applies(p.plan, p.M, p.K, p.nnz, p.sw) && buf_gathers_ok(p, 4)) {
       Problem q = p;
       sweep_geometry(p.K, p.sw, q.sweep_shift, q.sweep_bands);
       return launch_rg<4, 16, 1, kVec4U, LDS, CSRSPMM_SWEEP_SU, true, true>(q, s);
