@@ -17,7 +17,10 @@ stream.  Prints ONE JSON line:
              once) and the gather-model figure (a full B row per nonzero,
              above 1 when B is served from L2 or the MALL).  traffic.json
              records the kernel-source digest it was measured on; a
-             mismatch with the sources being benched is flagged
+             mismatch with the sources being benched is flagged.  Also from
+             traffic.json: the L2 (TCC) busy fraction of the main kernel and
+             of the whole call (TCC_BUSY_avr over GRBM_GUI_ACTIVE per XCD),
+             the bound these gather kernels run against
   modes      per-call median and mean of the headline variant timed alone:
              warm (back to back), api (host clock with a device sync, as the
              reference's spmm() pays) and cold (after a 512 MiB scratch write
@@ -113,6 +116,8 @@ def figures(cfg, a, ms, main_ms, traffic_file, key=None, bmin=None, balg=None):
             f["measured_gbs"] = round(gbs, 1)
             f["measured_frac"] = round(gbs / HBM_PEAK_GBS, 4)
             f["traffic_current"] = fresh
+            if e.get("l2_busy_main") is not None:
+                f["l2_busy_main"] = e["l2_busy_main"]
     return f
 
 
@@ -417,7 +422,11 @@ def main():
         "compulsory_frac": round(bmin / t_s / 1e9 / HBM_PEAK_GBS, 4),
         "gather_model_bytes": balg,
         "gather_model_gbs": round(balg / t_s / 1e9, 1),
-        "kernel": f"{resolved}: all launches of one call", "kernel_ms": round(main_ms, 5)}
+        "kernel": f"{resolved}: all launches of one call", "kernel_ms": round(main_ms, 5),
+        # the bound the counters show: the main kernel's L2 (TCC) busy fraction
+        "l2_busy_main": tr.get("l2_busy_main") if tr else None,
+        "l2_busy_main_kernel": tr.get("l2_busy_main_kernel") if tr else None,
+        "l2_busy_call": tr.get("l2_busy_call") if tr else None}
     if traffic is not None and not tr_fresh:
         print("[bench] WARNING: profiles/traffic.json was measured on other kernel sources "
               f"({roofline['traffic_source_digest']} vs {roofline['kernel_source_digest']})",

@@ -6,10 +6,11 @@
 #   bash csrspmm_amd/profile_configs.sh NAME:CONFIG:ALGO[:plan|:nopanels] ...
 #   bash csrspmm_amd/profile_configs.sh bench     # the default bench run, traced
 #
-# Per spec, four runs of csrspmm_amd/profile_run.py: a kernel trace with
+# Per spec, five runs of csrspmm_amd/profile_run.py: a kernel trace with
 # --stats (20 calls), FETCH_SIZE and WRITE_SIZE (3 calls each, with a 1 GiB
-# device copy that calibrates them), and TCC_HIT_sum TCC_MISS_sum VALUBusy
-# (3 calls).  Counters get runs of their own, never with a trace domain.
+# device copy that calibrates them), TCC_HIT_sum TCC_MISS_sum VALUBusy, and
+# TCC_BUSY_avr GRBM_GUI_ACTIVE TA_BUSY_avr (3 calls each).  Counters get runs
+# of their own, never with a trace domain.
 set -o pipefail
 cd /tmp && export TMPDIR=/tmp && cd "${GRAFT_REPO_ROOT:-$(dirname "$0")/..}" || exit 1
 OUT=gpurun_out/prof
@@ -39,4 +40,7 @@ for spec in "$@"; do
   echo "[profile] $name: hit rate, VALU busy"
   timeout -s KILL 120 rocprofv3 --pmc TCC_HIT_sum TCC_MISS_sum VALUBusy -d "$OUT/$name/hit" \
     -o "$name" --output-format csv -- $run --calls 3 > "$OUT/$name.hit.log" 2>&1 || exit 1
+  echo "[profile] $name: L2 and TA busy"
+  timeout -s KILL 120 rocprofv3 --pmc TCC_BUSY_avr GRBM_GUI_ACTIVE TA_BUSY_avr -d "$OUT/$name/busy" \
+    -o "$name" --output-format csv -- $run --calls 3 > "$OUT/$name.busy.log" 2>&1 || exit 1
 done

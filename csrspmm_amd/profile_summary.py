@@ -31,6 +31,7 @@ from . import configs
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 PEAK = 8.0e12
+XCDS = 8
 
 
 def short(n: str) -> str:
@@ -74,6 +75,9 @@ def _command(name, info, kind):
     if kind == "hit":
         return (f"rocprofv3 --pmc TCC_HIT_sum TCC_MISS_sum VALUBusy -d OUT/{name}/hit -o {name} "
                 f"--output-format csv -- {run} --calls 3")
+    if kind == "busy":
+        return (f"rocprofv3 --pmc TCC_BUSY_avr GRBM_GUI_ACTIVE TA_BUSY_avr -d OUT/{name}/busy "
+                f"-o {name} --output-format csv -- {run} --calls 3")
     d = kind.split("_")[0].lower()
     return (f"rocprofv3 --pmc {kind} -d OUT/{name}/{d} -o {name} --output-format csv -- {run} "
             f"--calls 3 --copy-mib 1024")
@@ -123,7 +127,8 @@ def summarize(prof: str, name: str):
         f"{name}:{info['cfg']}:{info['algo']}" + (f":{info['mode']}" if info["mode"] else "")
         + "` runs them):", "```",
         _command(name, info, "trace"), _command(name, info, "FETCH_SIZE"),
-        _command(name, info, "WRITE_SIZE"), _command(name, info, "hit"), "```", "",
+        _command(name, info, "WRITE_SIZE"), _command(name, info, "hit"),
+        _command(name, info, "busy"), "```", "",
         f"Kernel sources: digest `{info['digest']}` (csrspmm_amd.kernel_source_digest).", "",
         f"M={info['M']} nnz={info['nnz']} N={info['N']}, distinct columns U={info['U']}; per call: "
         f"gather-model bytes {info['balg']:,}, compulsory bytes {info['bmin']:,}.", "",
@@ -171,6 +176,34 @@ def summarize(prof: str, name: str):
         vb = sum(e["VALUBusy"]) / max(len(e["VALUBusy"]), 1)
         lines.append(f"| `{k}` | {h / 1e6:.2f} M | {m / 1e6:.2f} M | {h / max(h + m, 1):.3f} | "
                      f"{vb:.1f} |")
+    # L2 (TCC) and texture-address (TA) busy: each counter's mean over its
+    # instances, in cycles, over the dispatch's GRBM_GUI_ACTIVE cycles, which
+    # rocprofv3 sums over the 8 XCDs (divided by 8 it matches the kernel
+    # durations at the ~2.4 GHz clock)
+    busy = {}
+    for r in _rows(f"{d}/busy/*counter_collection.csv"):
+        if "csrspmm_hip" not in r["Kernel_Name"]:
+            continue
+        e = busy.setdefault(short(r["Kernel_Name"]), {})
+        e.setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+
+    def frac(e, c):
+        g = sum(e.get("GRBM_GUI_ACTIVE", [])) / XCDS
+        return sum(e.get(c, [])) / g if g > 0 else 0.0
+
+    lines += ["", "## L2 and TA busy per kernel (`--pmc TCC_BUSY_avr GRBM_GUI_ACTIVE TA_BUSY_avr`, "
+              "3 calls)", "",
+              "Busy cycles (mean over the TCC channels / TA units) over the dispatch's cycles "
+              "(GRBM_GUI_ACTIVE / 8 XCDs).  An L2 busy near 1 is the L2's request rate, the "
+              "bound of a gather kernel whose B rows come from L2 and the MALL.", "",
+              "| kernel | GRBM cycles per XCD | L2 (TCC) busy | TA busy |", "|---|---|---|---|"]
+    for k, e in busy.items():
+        g = sum(e.get("GRBM_GUI_ACTIVE", [])) / max(len(e.get("GRBM_GUI_ACTIVE", [])), 1) / XCDS
+        lines.append(f"| `{k}` | {g:,.0f} | {frac(e, 'TCC_BUSY_avr'):.3f} | "
+                     f"{frac(e, 'TA_BUSY_avr'):.3f} |")
+    main_k = max(busy, key=lambda k: sum(busy[k].get("GRBM_GUI_ACTIVE", [0])), default=None)
+    tot_g = sum(sum(e.get("GRBM_GUI_ACTIVE", [])) for e in busy.values()) / XCDS
+    tot_b = sum(sum(e.get("TCC_BUSY_avr", [])) for e in busy.values())
     with open(os.path.join(ROOT, "profiles", name + ".md"), "w") as f:
         f.write("\n".join(lines) + "\n")
     key = {"plan": f"{info['cfg']}/plan{info['algo']}",
@@ -180,7 +213,10 @@ def summarize(prof: str, name: str):
              "fetch_factor": round(ff, 4), "write_factor": round(wf, 4),
              "spmm_us_per_call": round(per_call_us, 1), "bytes_alg": info["balg"],
              "bytes_min": info["bmin"], "source_digest": info["digest"], "summary": f"{name}.md",
-             "kernels": [short(r["Name"]) for r in spmm]}
+             "kernels": [short(r["Name"]) for r in spmm],
+             "l2_busy_main": round(frac(busy[main_k], "TCC_BUSY_avr"), 4) if main_k else None,
+             "l2_busy_main_kernel": main_k,
+             "l2_busy_call": round(tot_b / tot_g, 4) if tot_g > 0 else None}
     print(f"{name}: {per_call_us:.1f} us, measured {tr / t / PEAK:.3f} of peak, "
           f"compulsory {info['bmin'] / t / PEAK:.3f}, sources {info['digest']}")
     return key, entry
