@@ -52,6 +52,7 @@ HIP_API = {
     "csrspmm_plan_algorithm": (_c_int, [_c_void_p]),
     "csrspmm_plan_device_bytes": (_c_size_t, [_c_void_p]),
     "csrspmm_plan_panelized_rows": (_c_int, [_c_void_p]),
+    "csrspmm_plan_shares": (_c_int, [_c_void_p, _c_int]),
     "csrspmm_plan_destroy": (_c_int, [_c_void_p]),
     "csrspmm_release_workspace": (_c_int, [_c_void_p]),
     "csrspmm_release_all_workspaces": (_c_int, []),
@@ -255,6 +256,13 @@ class Plan:
     @property
     def panelized_rows(self) -> int:
         return hip().csrspmm_plan_panelized_rows(self._h)
+
+    def shares(self, N) -> bool:
+        """Whether this plan's calls of N columns split long rows by XCD."""
+        st = hip().csrspmm_plan_shares(self._h, int(N))
+        if st < 0:
+            raise RuntimeError(f"csrspmm_plan_shares: status {st}")
+        return bool(st)
 
     def spmm(self, B, C, alpha, beta, flags=0, stream=None):
         if stream is None:

@@ -105,7 +105,7 @@ struct csrspmm_plan_s {
   void* d_ws = nullptr;
   size_t ws_bytes = 0;
   int tab_n = 0, tab_vec = 0, tab_P = -1;
-  bool tab_sliced = false;
+  bool tab_sliced = false, tab_shares = false;
   WorkspaceLayout tab_L{};
   int dev_nl = 0;  // rows the device schedule panelized
   // partial buffers, grown with N
@@ -339,6 +339,16 @@ void call_slicing(const csrspmm_plan_s* p, int vec, int N, int P, int& sw, bool&
   if (xslice) sw = kSliceWidth;
 }
 
+// XCD shares of a call of N without panels: the per-call rule, with the
+// plan's true longest row as the hint.
+bool device_shares(const csrspmm_plan_s* p, int vec, int N) {
+  if (device_panels(p, vec, N) > 0) return false;
+  int sw;
+  bool xslice;
+  call_slicing(p, vec, N, 0, sw, xslice);
+  return share_applies(true, p->K, N, p->nnz, sw, 0, p->maxlen);
+}
+
 // A Problem carrying the plan's CSR and tables (B and C are the call's); the
 // merge blocks are the per-call path's for the tables' slicing.
 void bind_tables(const csrspmm_plan_s* p, Problem& q, int vec) {
@@ -351,7 +361,8 @@ void bind_tables(const csrspmm_plan_s* p, Problem& q, int vec) {
 // plan's workspace: plan_kernel and the panel schedule, on stream s.
 hipError_t build_device_tables(csrspmm_plan_s* p, int N, int vec, hipStream_t s) {
   const int P = device_panels(p, vec, N);
-  const WorkspaceLayout L = workspace_layout(p->M, p->K, N, p->nnz, P);
+  const bool shares = P == 0 && device_shares(p, vec, N);
+  const WorkspaceLayout L = workspace_layout(p->M, p->K, N, p->nnz, P, shares);
   hipError_t e = hipSuccess;
   if (L.total > p->ws_bytes) {
     e = hipStreamSynchronize(s);  // earlier calls may still use the old tables
@@ -374,6 +385,7 @@ hipError_t build_device_tables(csrspmm_plan_s* p, int N, int vec, hipStream_t s)
   bool xslice;
   call_slicing(p, vec, N, P, sw, xslice);
   p->tab_sliced = sw > 0 && !xslice;  // XCD slices keep the unsliced merge blocks
+  p->tab_shares = shares;
   Problem q{};
   q.M = p->M;
   q.K = p->K;
@@ -436,7 +448,9 @@ int csrspmm_plan_create(int algo, int M, int K, int nnz, const int* rowptr, cons
                      concrete == CSRSPMM_ALGO_WARP_PER_ROW_SMEM_FP4) && n_eff % 4 == 0 ? 4 : 1;
     p->maxlen = maxlen;
     p->use_plan = ((long long)M + nnz >= kPlanMinItems) || maxlen > kSegLen;
-    p->dev_mode = p->use_plan && device_panels(p, vec, n_eff) > 0;
+    // per-call tables built once: with column panels, or with XCD shares
+    // (the host-built tables have neither share entries nor boundaries)
+    p->dev_mode = p->use_plan && (device_panels(p, vec, n_eff) > 0 || device_shares(p, vec, n_eff));
     if (p->dev_mode) {
       e = build_device_tables(p, n_eff, vec, static_cast<hipStream_t>(stream));
       if (e != hipSuccess) {
@@ -485,9 +499,10 @@ int csrspmm_plan_spmm_f32(csrspmm_plan_t plan, int N, const float* B, long long 
     int sw;
     bool xslice;
     call_slicing(p, vec, N, P, sw, xslice);
+    const bool shares = P == 0 && device_shares(p, vec, N);
     const long long ldp = ((long long)N + 3) & ~3LL;
     if (P != p->tab_P || vec != p->tab_vec || (sw > 0 && !xslice) != p->tab_sliced ||
-        ldp > p->tab_L.ldp) {
+        shares != p->tab_shares || ldp > p->tab_L.ldp) {
       const hipError_t eb = build_device_tables(p, N, vec, s);
       if (eb != hipSuccess) return eb == hipErrorOutOfMemory ? CSRSPMM_STATUS_ALLOC_FAILED : (int)eb;
     }
@@ -555,6 +570,15 @@ int csrspmm_plan_algorithm(csrspmm_plan_t plan) { return plan ? plan->algo : -1;
 
 size_t csrspmm_plan_device_bytes(csrspmm_plan_t plan) {
   return plan ? plan->dev.bytes + plan->partial_bytes + plan->ws_bytes : 0;
+}
+
+int csrspmm_plan_shares(csrspmm_plan_t plan, int N) {
+  if (!plan || N <= 0) return CSRSPMM_STATUS_INVALID_VALUE;
+  const csrspmm_plan_s* p = plan;
+  if (!p->dev_mode || !is_rowgroup_algorithm(p->algo)) return 0;
+  const int vec = (p->algo == CSRSPMM_ALGO_WARP_PER_ROW_FP4 ||
+                   p->algo == CSRSPMM_ALGO_WARP_PER_ROW_SMEM_FP4) && N % 4 == 0 ? 4 : 1;
+  return device_shares(p, vec, N) ? 1 : 0;
 }
 
 int csrspmm_plan_panelized_rows(csrspmm_plan_t plan) {

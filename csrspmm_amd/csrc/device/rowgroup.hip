@@ -1657,6 +1657,7 @@ hipError_t launch_share_bounds(const Problem& p, hipStream_t s) {
 hipError_t launch_plan_tables(const Problem& p, hipStream_t s) {
   hipLaunchKernelGGL(plan_kernel, dim3(plan_blocks(p)), dim3(256), 0, s, p);
   if (p.dp.P > 0) return launch_panel_schedule(p, s);
+  if (p.plan && p.nslots > 0 && p.shares) return launch_share_bounds(p, s);
   return hipGetLastError();
 }
 
@@ -1673,7 +1674,7 @@ static hipError_t launch_rowgroup_all(const Problem& p, int vec, bool lds, hipSt
     if (e != hipSuccess) return e;
   }
   const bool shares = p.plan && p.nslots > 0 && p.shares;
-  if (shares) {
+  if (shares && !p.dp_ready) {
     e = launch_share_bounds(p, s);
     if (e != hipSuccess) return e;
   }

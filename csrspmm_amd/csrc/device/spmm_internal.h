@@ -447,8 +447,8 @@ struct Problem {
   // are sorted and in range (plan_kernel sets it from rowptr,
   // panel_window_kernel clears it), else 0.
   unsigned char* dp_flag;
-  // A stored plan built the per-call panel schedule (dp) once: no panel
-  // schedule launches per call.
+  // A stored plan built the per-call panel schedule (dp), or the XCD share
+  // entries, once: no panel schedule or share-bounds launches per call.
   bool dp_ready;
   // Band sweep of the short rows of a column slice (sweep_geometry; bands 0:
   // merge blocks instead): bands of 2^sweep_shift B rows, sweep_bands of them.

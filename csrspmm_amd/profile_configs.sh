@@ -19,7 +19,7 @@ for spec in "$@"; do
   if [ "$spec" = bench ]; then
     echo "[profile] bench trace"
     timeout -k 10 300 rocprofv3 --kernel-trace --stats -d "$OUT/bench_xl/trace" -o bench_xl \
-      --output-format csv -- python3 bench.py --cpu-seconds 0 --variants none --plan-algo none \
+      --output-format csv -- python3 bench.py --cpu-seconds 0 --variants none --plan-algo none --configs none \
       > "$OUT/bench_xl.log" 2>&1 || exit 1
     continue
   fi

@@ -235,7 +235,7 @@ def summarize_bench(prof: str):
         "Command (repository root on the MI355X box; `bash csrspmm_amd/profile_configs.sh "
         "bench` runs it):", "```",
         "rocprofv3 --kernel-trace --stats -d OUT/bench_xl/trace -o bench_xl --output-format csv "
-        "-- python3 bench.py --cpu-seconds 0 --variants none --plan-algo none", "```", "",
+        "-- python3 bench.py --cpu-seconds 0 --variants none --plan-algo none --configs none", "```", "",
         f"bench.py times {j['warmup']} warmup + {j['steps']} timed calls (plus its timing-mode "
         "calls); its live HIP-event figure for one call (`roofline.kernel_ms`) should match the "
         "per-call sum of the SpMM kernels below.", "",

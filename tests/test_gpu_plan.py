@@ -34,12 +34,24 @@ def test_plan_configs(cfg_name, algo, gpu):
         assert plan.algorithm in ("WarpPerRowFp4", "WarpPerRowSmemFp4", "WarpPerRowSmem")
     rows = sample_rows(a, cfg_name in ("host", "medium"))
     concrete = plan.algorithm
+    shares = plan.shares(cfg.N)
+    # a plan splits long rows by XCD where the per-call path would, with its
+    # true longest row as the hint (R-MAT at N = 64 and 512, scalar columns)
+    assert shares == capi.call_shares(concrete, a.M, a.K, cfg.N, a.nnz, int(np.diff(a.rowptr).max()))
+    if cfg_name in ("rmat", "rmat512") and concrete == "WarpPerRowSmem":
+        assert shares
     C1 = plan_run(plan, B, gpu, a.M, cfg.N)
     assert not np.isnan(C1).any()
     assert_parity(concrete, C1, a.rowptr, a.colidx, a.vals, B, None, 1.0, 0.0, rows=rows,
-                  what=f"plan {cfg_name}", shares=False)
+                  what=f"plan {cfg_name}", shares=shares)
     C2 = plan_run(plan, B, gpu, a.M, cfg.N)
     assert np.array_equal(C1.view(np.uint32), C2.view(np.uint32))  # deterministic, reusable
+    if shares:
+        # the same tables as a per-call product with the hint: the same bits
+        from test_gpu_parity import run_spmm
+        Cc = run_spmm(concrete, a.rowptr, a.colidx, a.vals, B, gpu,
+                      hint=int(np.diff(a.rowptr).max()))
+        assert np.array_equal(C1.view(np.uint32), Cc.view(np.uint32)), "plan and per-call differ"
     if cfg_name == "xl":
         # at N = 128 the warp-per-row forms, float4 and scalar, panelize XL's
         # 1501 rows of >= 1024 nonzeros; Naive has no plan to panelize
@@ -60,10 +72,10 @@ def test_plan_epilogues_and_growth(gpu):
         rows = sample_rows(a, False)
         C = plan_run(plan, B, gpu, a.M, N, C0=C0, alpha=0.5, beta=-2.0)
         assert_parity(plan.algorithm, C, a.rowptr, a.colidx, a.vals, B, C0, 0.5, -2.0, rows=rows,
-                      what=f"plan beta N={N}", shares=False)
+                      what=f"plan beta N={N}", shares=plan.shares(N))
         C = plan_run(plan, B, gpu, a.M, N, alpha=1.5, beta=0.25, flags=capi.FLAG_C_IS_ZERO)
         assert_parity(plan.algorithm, C, a.rowptr, a.colidx, a.vals, B, None, 1.5, 0.25,
-                      rows=rows, c0_zero=True, what=f"plan c_is_zero N={N}", shares=False)
+                      rows=rows, c0_zero=True, what=f"plan c_is_zero N={N}", shares=plan.shares(N))
     plan.close()
 
 
