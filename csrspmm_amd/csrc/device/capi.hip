@@ -201,9 +201,31 @@ int free_owned_device_synced(int dev, OwnedWorkspace& w) {
   return (int)e3;
 }
 
+// Grows w to at least `bytes` (caller holds w.m).
+int grow_locked(OwnedWorkspace& w, void* stream, size_t bytes) {
+  if (w.bytes >= bytes) return 0;
+  if (w.ptr) {
+    hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return (int)e;
+    e = hipFree(w.ptr);
+    w.ptr = nullptr;
+    w.bytes = 0;
+    if (e != hipSuccess) return (int)e;
+  }
+  const size_t want = bytes + bytes / 4;  // headroom against repeated small growth
+  if (hipMalloc(&w.ptr, want) != hipSuccess) {
+    w.ptr = nullptr;
+    (void)hipGetLastError();
+    return CSRSPMM_STATUS_ALLOC_FAILED;
+  }
+  w.bytes = want;
+  return 0;
+}
+
 // The workspace of (current device, stream), grown to at least `bytes`, in
-// *out; it stays locked through `lock` (and alive through `held`) until the
-// caller has enqueued the kernels that use it.
+// *out; on success it stays locked through `lock` (and alive through `held`)
+// until the caller has enqueued the kernels that use it, on failure it is
+// unlocked.
 int owned_workspace(void* stream, size_t bytes, void** out, std::shared_ptr<OwnedWorkspace>& held,
                     std::unique_lock<std::mutex>& lock) {
   int dev = 0;
@@ -237,23 +259,11 @@ int owned_workspace(void* stream, size_t bytes, void** out, std::shared_ptr<Owne
     lock.unlock();  // evicted or released between the lookup and the lock
   }
   OwnedWorkspace& w = *held;
-  if (w.bytes < bytes) {
-    if (w.ptr) {
-      e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
-      if (e != hipSuccess) return (int)e;
-      e = hipFree(w.ptr);
-      w.ptr = nullptr;
-      w.bytes = 0;
-      if (e != hipSuccess) return (int)e;
-    }
-    const size_t want = bytes + bytes / 4;  // headroom against repeated small growth
-    e = hipMalloc(&w.ptr, want);
-    if (e != hipSuccess) {
-      w.ptr = nullptr;
-      (void)hipGetLastError();
-      return CSRSPMM_STATUS_ALLOC_FAILED;
-    }
-    w.bytes = want;
+  const int st = grow_locked(w, stream, bytes);
+  if (st != 0) {
+    // unlocked on failure: the caller may retry with a smaller size
+    lock.unlock();
+    return st;
   }
   *out = w.ptr;
   return 0;
