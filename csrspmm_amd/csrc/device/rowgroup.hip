@@ -771,6 +771,21 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(SWE
     c_lo = (slice0 + local) * p.sw;
     c_hi = min(p.N, c_lo + p.sw);
   }
+  if constexpr (!PIECES) {
+    // The segment blocks come after the merge blocks of their slice in the
+    // grid (rowgroup_block numbers them first): on a matrix without long
+    // rows they only find empty slots, and first they held dispatch slots
+    // the merge blocks were waiting for.  Measured on MI355X per call
+    // (bit-identical): large 4 x 74.2 -> 72.3 us, medium main kernel 40.7 ->
+    // 40.2 us, with a base-size workspace (no panels, no shares) R-MAT
+    // WarpPerRowSmem 590 -> 552 us and WarpPerRowFp4 613 -> 579, XL-98
+    // 1816 -> 1795; XL WarpPerRowFp4 without panels 631 -> 651.  The pieces
+    // kernels interleave the roles instead (interleave_roles).
+    if (seg_blocks > 0) {
+      const int units = slice_blocks - seg_blocks;
+      bid = bid >= units ? bid - units : bid + seg_blocks;
+    }
+  }
   rowgroup_block<VEC, G, T, U, LDS, BUF, SU, SWEEP>(p, bid, seg_blocks, c_lo, c_hi, gl, gbase, gid, stage,
                                                      sweep_bnd);
 }

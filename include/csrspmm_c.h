@@ -305,11 +305,11 @@ int csrspmm_plan_algorithm(csrspmm_plan_t plan);
 size_t csrspmm_plan_device_bytes(csrspmm_plan_t plan);
 /* Rows the plan cut into column panels. */
 int csrspmm_plan_panelized_rows(csrspmm_plan_t plan);
-/* 1 when the plan's calls of N columns split their long rows by XCD (as
- * csrspmm_call_shares reports for a per-call product, with the plan's true
- * longest row as the hint): rows above 128 nonzeros are then summed in parts
- * rather than in CSR order.  0 otherwise; a negative status for a null plan
- * or N <= 0.  No counterpart in the reference: a query for tests and tools,
+/* 1 when the plan's calls of N columns (16-byte aligned B and C rows) split
+ * their long rows by XCD (as csrspmm_call_shares reports for a per-call
+ * product, with the plan's true longest row as the hint): rows above 128
+ * nonzeros are then summed in parts rather than in CSR order.  0 otherwise;
+ * a negative status for a null plan or N <= 0.  No counterpart in the reference: a query for tests and tools,
  * like csrspmm_plan_panelized_rows. */
 int csrspmm_plan_shares(csrspmm_plan_t plan, int N);
 /* Waits for the device, then frees the plan (NULL is a no-op). */
