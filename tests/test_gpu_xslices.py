@@ -116,3 +116,28 @@ def test_combine_single_long_row(algo, where, gpu):
     print(f"[combine] {algo} {where} M={M} nnz={colidx.size} long row {row}", flush=True)
     C = run(algo, rowptr, colidx, vals, B, gpu)
     check(algo, C, rowptr, colidx, vals, B, what=f"long row {where}")
+
+
+@pytest.mark.parametrize("algo", ["WarpPerRowFp4", "Auto"])
+def test_xslices_plan_across_widths(algo, gpu):
+    """One stored plan (hinted at N = 64, no XCD slices) called at N = 128
+    and 256 (two and four XCD bands) and 512 (ordinary column slices), with
+    a long row among short ones: each call bit-identical to the per-call
+    product and within the oracle's bar."""
+    K, M = 16384, 5000
+    lens = np.random.default_rng(13).integers(10, 120, M)
+    lens[1234] = 6000  # a long row: segments and the combine
+    rowptr, colidx, vals = csr_from_lengths(lens, K, seed=13)
+    plan = capi.Plan(algo, t(rowptr, gpu), t(colidx, gpu), t(vals, gpu), K, n_hint=64)
+    for N in (128, 256, 512, 64):
+        B = gen.dense(N + 1, gen.TAG_B, K, N)
+        dC = torch.full((M, N), float("nan"), device=gpu)
+        plan.spmm(t(B, gpu), dC, 1.0, 0.0)
+        torch.cuda.synchronize()
+        Cp = dC.cpu().numpy()
+        Cc = run(plan.algorithm, rowptr, colidx, vals, B, gpu)
+        check(plan.algorithm, Cp, rowptr, colidx, vals, B, what=f"plan N={N}")
+        short = np.diff(rowptr) <= 128
+        assert np.array_equal(Cp[short].view(np.uint32), Cc[short].view(np.uint32)), \
+            f"N={N}: plan and per-call differ on rows summed whole"
+    plan.close()
