@@ -12,7 +12,8 @@ stream.  Prints ONE JSON line:
              WRITE_SIZE, calibrated on a device copy: profiles/traffic.json)
              over the GPU time of that call (a HIP event pair around all of
              the call's launches, recorded by the library on the launch
-             stream, csrspmm_timing_*), against 8 TB/s.  Beside it, never in
+             stream, csrspmm_timing_*, on every TIMING_EVERY-th call of the
+             timed loop), against 8 TB/s.  Beside it, never in
              its place: the compulsory fraction (each distinct B row read
              once) and the gather-model figure (a full B row per nonzero,
              above 1 when B is served from L2 or the MALL).  traffic.json
@@ -143,6 +144,14 @@ def config_leg(capi, torch, name, dev, args):
     return out
 
 
+# The library's span events are recorded on one call in TIMING_EVERY of a
+# timed loop: each recording adds two marker packets to the stream, which cost
+# about 8 us of GPU time per call on medium (48.4 against 40.6 us per call
+# back to back), so recording every call inflated the per-call times of the
+# short configs.
+TIMING_EVERY = 8
+
+
 def time_variant(capi, torch, algo, d, steps, warmup):
     """(ms per call, main-kernel ms per call)."""
     stream = torch.cuda.current_stream()
@@ -151,12 +160,12 @@ def time_variant(capi, torch, algo, d, steps, warmup):
                   workspace=d["ws"])
     torch.cuda.synchronize()
     capi.timing_read()  # drop warmup recordings
-    capi.timing_enable(True)
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record(stream)
-    for _ in range(steps):
+    for i in range(steps):
+        capi.timing_enable(i % TIMING_EVERY == 0)
         capi.spmm(algo, d["rowptr"], d["colidx"], d["vals"], d["B"], d["C"], 1.0, 0.0,
                   workspace=d["ws"])
     stop.record(stream)
@@ -221,12 +230,12 @@ def time_plan(capi, torch, algo, d, K, N, steps, warmup):
         plan.spmm(d["B"], d["C"], 1.0, 0.0)
     torch.cuda.synchronize()
     capi.timing_read()
-    capi.timing_enable(True)
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
     stream = torch.cuda.current_stream()
     start.record(stream)
-    for _ in range(steps):
+    for i in range(steps):
+        capi.timing_enable(i % TIMING_EVERY == 0)
         plan.spmm(d["B"], d["C"], 1.0, 0.0)
     stop.record(stream)
     torch.cuda.synchronize()

@@ -39,6 +39,8 @@ WorkspaceLayout workspace_layout(int M, int K, int N, int nnz, int P, bool share
   off = align256(off + (size_t)(nnz >> g.seg_shift) * (size_t)L.ldp * sizeof(float));
   L.need_off = off;
   off = align256(off + (size_t)plan_row_blocks(M));
+  L.segcnt_off = off;
+  off = align256(off + (size_t)L.nslots * sizeof(int));
   L.base_total = off;
   if (P > 0 && K > 0) {
     const long long w = ((long long)K + P - 1) / P;
@@ -86,6 +88,7 @@ void bind_workspace(Problem& p, void* ws, const WorkspaceLayout& L, int mblk) {
   p.partials = reinterpret_cast<float*>(b + L.partials_off);
   p.need = reinterpret_cast<unsigned char*>(b + L.need_off);
   p.need_blocks = plan_row_blocks(p.M);
+  p.seg_cnt = reinterpret_cast<int*>(b + L.segcnt_off);
   p.ldp = L.ldp;
   p.nslots = L.nslots;
   p.mblk = mblk;

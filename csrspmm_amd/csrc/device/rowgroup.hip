@@ -85,6 +85,12 @@ constexpr int kPiecesPerGroup = CSRSPMM_PIECES_PER_GROUP;
 #define CSRSPMM_SWEEP_WPE 8
 #endif
 
+// Split rows summed in the main launch (Problem::seg_fuse); 0: always the
+// combine launch.
+#ifndef CSRSPMM_SEG_FUSE
+#define CSRSPMM_SEG_FUSE 1
+#endif
+
 // B-row gathers in flight per lane in the pieces kernel; build-time tunable.
 #ifndef CSRSPMM_PIECE_UNROLL
 #define CSRSPMM_PIECE_UNROLL 4
@@ -580,10 +586,63 @@ __device__ __forceinline__ void pieces_body(const Problem& p, int block, int gl,
   }
 }
 
+// Split rows summed in the main launch (Problem::seg_fuse).  A segment's
+// partial row is stored, and the last segment's group reads the row's
+// partials, with agent-scope atomic stores and loads (sc1: past this XCD's
+// L2 to where every XCD sees them), and the stores are complete (vmcnt 0)
+// before the segment counts itself, so the last count finds every partial.
+__device__ __forceinline__ void store_partial(float* dst, f4 v) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) __hip_atomic_store(dst + i, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_partial(float* dst, float v) {
+  __hip_atomic_store(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Column `col` of a row's n partial rows at `base`, added in the combine's
+// order for P lane groups (combine_kernel: group q sums partials q, q + P,
+// ... in turn from zero, then the groups are added pairwise, xor 1, 2, 4),
+// so a fused row is bit for bit the combined one.  One column and one
+// partial at a time keeps the registers this cold path adds to the main
+// kernels few.
+__device__ __forceinline__ float strided_sum(const float* base, int q, int P, int n, long long ldp) {
+  float v = 0.0f;
+#pragma unroll 1
+  for (int k = q; k < n; k += P)
+    v += __hip_atomic_load(base + (long long)k * ldp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return v;
+}
+__device__ __forceinline__ float partial_tree(const float* base, int P, int n, long long ldp) {
+  if (P == 1) return strided_sum(base, 0, 1, n, ldp);
+  if (P == 2) return strided_sum(base, 0, 2, n, ldp) + strided_sum(base, 1, 2, n, ldp);
+  float a = strided_sum(base, 0, P, n, ldp) + strided_sum(base, 1, P, n, ldp);
+  a = a + (strided_sum(base, 2, P, n, ldp) + strided_sum(base, 3, P, n, ldp));
+  if (P == 4) return a;
+  float b = strided_sum(base, 4, P, n, ldp) + strided_sum(base, 5, P, n, ldp);
+  b = b + (strided_sum(base, 6, P, n, ldp) + strided_sum(base, 7, P, n, ldp));
+  return a + b;
+}
+
+// The whole of a split row from its n partial rows at `base` (every
+// column; C row at crow), by the G lanes of the group whose segment counted
+// last.  P follows the combine's lane groups for this N (launch_combine:
+// ceil(N / 4) float4 chunks in groups of 8, 16, 32 or 64 lanes); the
+// epilogue is the combine's, element by element.
+__device__ __forceinline__ void fused_row_sum(float* crow, const float* base, int n, long long ldp, int N,
+                                              int epi, float alpha, float beta, int gl, int G) {
+  const int chunks = (N + 3) / 4;
+  const int P = chunks <= 8 ? 8 : chunks <= 16 ? 4 : chunks <= 32 ? 2 : 1;
+#pragma unroll 1
+  for (int c = gl; c < N; c += G) {
+    const float v = partial_tree(base + c, P, n, ldp);
+    st_c(crow + c, epi1(epi, alpha, beta, v, crow + c));
+  }
+}
+
 // One block's share of the main launch, over the columns [c_lo, c_hi):
 // block bid < seg_blocks takes long-row segment slots, the others merge
 // blocks of short rows (or, without a plan, rows).
-template <int VEC, int G, int T, int U, bool LDS, bool BUF, int SU, bool SWEEP>
+template <int VEC, int G, int T, int U, bool LDS, bool BUF, int SU, bool SWEEP, bool FUSE>
 __device__ __forceinline__ void rowgroup_block(const Problem& p, int bid, int seg_blocks, int c_lo,
                                                int c_hi, int gl, int gbase, int gid, int2* stage,
                                                int* sweep_bnd) {
@@ -592,15 +651,17 @@ __device__ __forceinline__ void rowgroup_block(const Problem& p, int bid, int se
   constexpr int PW = G * VEC * T;
   if (bid < seg_blocks) {
     // Long-row segments, one slot per group (grid-strided if the segment
-    // blocks are capped).
+    // blocks are capped).  FUSE: the last segment of a split row to finish
+    // (in every column slice) notes the row in fuse_row, and its group sums
+    // the row once the gathers are done.
     constexpr int US = SU > U ? (SU < G ? SU : G) : U;
-    for (int s = bid * GPB + gid; s < p.nslots; s += seg_blocks * GPB) {
+    auto slot = [&](int s, int& fuse_row, int& fuse_n, int& fuse_x0) {
       const int2 si = p.seg_info[s];
-      if (si.x < 0 || si.x >= p.M) continue;  // unused slot
+      if (si.x < 0 || si.x >= p.M) return;  // unused slot
       const int rs = p.rowptr[si.x];
       const int re = p.rowptr[si.x + 1];
       const int len = re - rs;
-      if (len >= kPanelMinLen && is_panelized(p, rs)) continue;  // summed by the pieces kernel
+      if (len >= kPanelMinLen && is_panelized(p, rs)) return;  // summed by the pieces kernel
       const int nseg = seg_count(p, len);
       const int start = rs + seg_begin(len, nseg, si.y);
       const int end = rs + seg_begin(len, nseg, si.y + 1);
@@ -619,6 +680,11 @@ __device__ __forceinline__ void rowgroup_block(const Problem& p, int bid, int se
                                             });
         if (nseg == 1) {  // the whole row: epilogue and store here
           store_row<VEC, T>(p, si.x, pn.col, pn.cval, acc);
+        } else if constexpr (FUSE) {
+#pragma unroll
+          for (int t = 0; t < T; ++t) {
+            if (pn.cval[t]) store_partial(prow + pn.col[t], acc[t]);
+          }
         } else {
 #pragma unroll
           for (int t = 0; t < T; ++t) {
@@ -626,6 +692,41 @@ __device__ __forceinline__ void rowgroup_block(const Problem& p, int bid, int se
           }
         }
       }
+      if constexpr (FUSE) {
+        // The wait also keeps the compiler from holding the row's values
+        // across the gathers above (they are read again).
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this group's partials are stored
+        const int row = p.seg_info[s].x;
+        const int r0 = p.rowptr[row];
+        const int n = seg_count(p, p.rowptr[row + 1] - r0);
+        if (n > 1) {
+          // every segment of the row in every column slice counts once
+          const int ns = p.sw > 0 ? (p.N + p.sw - 1) / p.sw : 1;
+          const int x0 = clamp_nnz(r0, p.nnz);
+          int seen = 0;
+          if (gl == 0)
+            seen = __hip_atomic_fetch_add(p.seg_cnt + (x0 >> p.slot_shift), 1, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+          seen = group_bcast<G>(seen, gbase, 0);
+          if (seen == n * ns - 1) {
+            fuse_row = row;
+            fuse_n = n;
+            fuse_x0 = x0;
+          }
+        }
+      }
+    };
+    int fuse_row = -1, fuse_n = 0, fuse_x0 = 0;
+    if constexpr (FUSE) {
+      // one slot per group: a fused launch's segment blocks are not capped
+      // (launch_rowgroup_all)
+      const int s = bid * GPB + gid;
+      if (s < p.nslots) slot(s, fuse_row, fuse_n, fuse_x0);
+      if (fuse_row >= 0)
+        fused_row_sum(p.C + (long long)fuse_row * p.ldc, p.partials + (long long)(fuse_x0 >> p.seg_shift) * p.ldp,
+                      fuse_n, p.ldp, p.N, p.epi, p.alpha, p.beta, gl, G);
+    } else {
+      for (int s = bid * GPB + gid; s < p.nslots; s += seg_blocks * GPB) slot(s, fuse_row, fuse_n, fuse_x0);
     }
     return;
   }
@@ -723,7 +824,7 @@ __device__ __forceinline__ void interleave_roles(int b, int piece_blocks, int to
 // column panels).  The kernels of calls without them are compiled without
 // that code, which as dead code cost the scalar N <= 64 kernel 9% on R-MAT
 // and the scalar N = 128 / 256 kernels 3-18% on the reference's sweep shapes.
-template <int VEC, int G, int T, int U, bool LDS, bool PIECES, int SU, bool BUF, bool SWEEP>
+template <int VEC, int G, int T, int U, bool LDS, bool PIECES, int SU, bool BUF, bool SWEEP, bool FUSE = false>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(SWEEP ? CSRSPMM_SWEEP_WPE : 1))) void rowgroup_kernel(Problem p, int piece_blocks,
                                                                 int seg_blocks, int slice_blocks,
                                                                 int slice0) {
@@ -786,7 +887,7 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(SWE
       bid = bid >= units ? bid - units : bid + seg_blocks;
     }
   }
-  rowgroup_block<VEC, G, T, U, LDS, BUF, SU, SWEEP>(p, bid, seg_blocks, c_lo, c_hi, gl, gbase, gid, stage,
+  rowgroup_block<VEC, G, T, U, LDS, BUF, SU, SWEEP, FUSE>(p, bid, seg_blocks, c_lo, c_hi, gl, gbase, gid, stage,
                                                      sweep_bnd);
 }
 
@@ -807,6 +908,7 @@ __device__ __forceinline__ void plan_row_entries(const Problem& p, int r, int b_
   for (int b = b_lo + first; b <= b_hi; b += step) p.block_start[b] = r;
   for (int s = s0 + first; s < s1; s += step)
     p.seg_info[s] = (s - s0) < nseg ? make_int2(r, s - s0) : make_int2(-1, 0);
+  if (p.seg_fuse && first == 0 && nseg >= 2 && s0 < s1) p.seg_cnt[s0] = 0;
   // the first window of a long row is the row's id
   for (int w = w0 + first; w < w1; w += step) {
     const int id = (w == w0 && x1 - x0 >= kPanelMinLen) ? 1 : 0;
@@ -1501,6 +1603,9 @@ hipError_t launch_rg(const Problem& p, hipStream_t s) {
       hipLaunchKernelGGL((rowgroup_kernel<VEC, G, T, U, LDS, kCanPanel, SU, BUF, false>), dim3((unsigned)blocks),
                          dim3(kWaves * 64), pad_lds, s, p, piece_blocks, seg_blocks, slice_blocks,
                          s0);
+    } else if (p.seg_fuse) {
+      hipLaunchKernelGGL((rowgroup_kernel<VEC, G, T, U, LDS, false, SU, BUF, SWEEP, true>), dim3((unsigned)blocks),
+                         dim3(kWaves * 64), pad_lds, s, p, 0, seg_blocks, slice_blocks, s0);
     } else {
       hipLaunchKernelGGL((rowgroup_kernel<VEC, G, T, U, LDS, false, SU, BUF, SWEEP>), dim3((unsigned)blocks),
                          dim3(kWaves * 64), pad_lds, s, p, 0, seg_blocks, slice_blocks, s0);
@@ -1681,7 +1786,18 @@ static hipError_t dispatch_main(const Problem& p, int vec, bool lds, hipStream_t
   return lds ? dispatch_vec1<true>(p, s) : dispatch_vec1<false>(p, s);
 }
 
-static hipError_t launch_rowgroup_all(const Problem& p, int vec, bool lds, hipStream_t s) {
+static hipError_t launch_rowgroup_all(const Problem& p_in, int vec, bool lds, hipStream_t s) {
+  // A per-call plan without column panels, XCD shares or stored panels sums
+  // its split rows in the main launch (Problem::seg_fuse), when every slot
+  // has a group of its own (the segment blocks, at least kWaves slots each,
+  // are not capped); a stored plan has no per-call plan_kernel to zero the
+  // counters, and keeps the combine.  Measured on MI355X per call (rocprof
+  // sums, bit-identical to the combine): medium 49.4 -> 44.6 us (the combine
+  // launch, which found no split row, gone), large 300.4 -> 300.0 us.
+  Problem p = p_in;
+  p.seg_fuse = CSRSPMM_SEG_FUSE && p.plan && !p.plan_ready && p.nslots > 0 && !p.no_split && !p.shares &&
+               p.npan == 0 && p.dp.P == 0 && p.seg_cnt != nullptr &&
+               (long long)p.nslots <= (long long)kSegBlocksMax * kWaves;
   if (p.plan && !p.plan_ready) hipLaunchKernelGGL(plan_kernel, dim3(plan_blocks(p)), dim3(256), 0, s, p);
   hipError_t e;
   if (p.dp.P > 0 && !p.dp_ready) {
@@ -1695,7 +1811,7 @@ static hipError_t launch_rowgroup_all(const Problem& p, int vec, bool lds, hipSt
   }
   e = dispatch_main(p, vec, lds, s);
   if (e != hipSuccess) return e;
-  if (p.plan && ((p.nslots > 0 && !p.no_split) || shares || p.npan > 0 || p.dp.P > 0)) {
+  if (p.plan && !p.seg_fuse && ((p.nslots > 0 && !p.no_split) || shares || p.npan > 0 || p.dp.P > 0)) {
     if (vec == 4) {
       launch_combine<4>(p, s);
     } else {

@@ -464,6 +464,13 @@ struct Problem {
   int* shr_cb;
   int4* shr_pb;
   float* shr_part;
+  // The split rows summed in the main launch (seg_fuse: a per-call plan
+  // with no column panels, XCD shares or stored panels): each segment of a
+  // split row counts itself in seg_cnt[the row's first slot], which
+  // plan_kernel zeroes, and the last of the row's segments (in every column
+  // slice) adds its partial rows, so no combine is launched.
+  bool seg_fuse;
+  int* seg_cnt;
 };
 
 // XCD shares.  On a B far larger than the L2s, with no column panels (hot
@@ -584,7 +591,7 @@ inline void set_row_hint(Problem& p, int max_row_nnz) {
 // Workspace layout for a problem (all offsets 256-byte aligned).  P > 0 adds
 // the per-call panel tables and partial buffer after the base sections.
 struct WorkspaceLayout {
-  size_t block_start_off, seg_info_off, partials_off, need_off, base_total;
+  size_t block_start_off, seg_info_off, partials_off, need_off, segcnt_off, base_total;
   size_t win_off, flag_off, pidx_off, list_off, bnd_off, sched_off, part_off, total;
   int nslots, nblocks;
   long long ldp;
