@@ -586,11 +586,87 @@ __device__ __forceinline__ void pieces_body(const Problem& p, int block, int gl,
   }
 }
 
+// Partials k = q, q + NG, q + 2*NG, ... (k < n) of one lane's four columns,
+// added in that order; partial k sits at src + idx(k) * ldp, idx(k) =
+// pieces[k] when a piece list is given, else k.  Partial rows are ldp = N
+// rounded up to 4 floats long and 256-byte aligned, so they are read as
+// float4 whatever the alignment of C.
+template <int NG>
+__device__ __forceinline__ f4 sum_strided(const float* src, const int* pieces, int n, int q,
+                                          long long ldp, bool cv) {
+  f4 acc = Vec<4>::zero();
+  if (!cv) return acc;
+  auto part = [&](int k) -> f4 {
+    const long long idx = pieces ? (long long)pieces[k] : (long long)k;
+    return *reinterpret_cast<const f4*>(src + idx * ldp);
+  };
+  int k = q;
+  for (; k + 7 * NG < n; k += 8 * NG) {
+    f4 a[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) a[u] = part(k + u * NG);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc = add_v(acc, a[u]);
+  }
+  for (; k < n; k += NG) acc = add_v(acc, part(k));
+  return acc;
+}
+
+// The value of lane (this lane ^ OFF), OFF in {8, 16, 32}: a DPP row_ror:8
+// (rotating a 16-lane row by half of it is the xor), a ds_swizzle swapping the
+// 16-lane halves of each 32-lane group (bit mode: and 0x1f, xor 0x10), and a
+// ds_bpermute across the 32-lane halves, which no gfx9 DPP or swizzle crosses.
+template <int OFF>
+__device__ __forceinline__ float lane_xor(float v) {
+  const int x = __builtin_bit_cast(int, v);
+  int y;
+  if constexpr (OFF == 8) {
+    y = __builtin_amdgcn_update_dpp(0, x, 0x128 /* row_ror:8 */, 0xF, 0xF, false);
+  } else if constexpr (OFF == 16) {
+    y = __builtin_amdgcn_ds_swizzle(x, 0x401F);
+  } else {
+    static_assert(OFF == 32, "lane_xor: offsets 8, 16, 32");
+    y = __builtin_amdgcn_ds_bpermute((lane_id() ^ 32) << 2, x);
+  }
+  return __builtin_bit_cast(float, y);
+}
+
+template <int OFF>
+__device__ __forceinline__ f4 add_lane_xor(f4 v) {
+  return f4{v.x + lane_xor<OFF>(v.x), v.y + lane_xor<OFF>(v.y), v.z + lane_xor<OFF>(v.z),
+            v.w + lane_xor<OFF>(v.w)};
+}
+
+// Sum over the 64 / GC lane groups of a wave by a fixed xor tree (offsets GC,
+// 2 GC, ... 32); every group ends with the total.  All lanes take part.
+template <int GC>
+__device__ __forceinline__ f4 wave_group_sum(f4 v) {
+  static_assert(GC == 8 || GC == 16 || GC == 32 || GC == 64, "group widths of the combine");
+  if constexpr (GC <= 8) v = add_lane_xor<8>(v);
+  if constexpr (GC <= 16) v = add_lane_xor<16>(v);
+  if constexpr (GC <= 32) v = add_lane_xor<32>(v);
+  return v;
+}
+
+// Columns c .. c + 3 of a C row (those below N): one float4 store when C
+// rows are 16-byte aligned (VEC == 4, N % 4 == 0), else one per column.
+template <int VEC>
+__device__ __forceinline__ void store_cols4(const Problem& p, float* cptr, int c, f4 v) {
+  if constexpr (VEC == 4) {
+    store_epi<4>(p, cptr, v);
+  } else {
+    store_epi<1>(p, cptr, v.x);
+    if (c + 1 < p.N) store_epi<1>(p, cptr + 1, v.y);
+    if (c + 2 < p.N) store_epi<1>(p, cptr + 2, v.z);
+    if (c + 3 < p.N) store_epi<1>(p, cptr + 3, v.w);
+  }
+}
+
 // Split rows summed in the main launch (Problem::seg_fuse).  A segment's
-// partial row is stored, and the last segment's group reads the row's
-// partials, with agent-scope atomic stores and loads (sc1: past this XCD's
-// L2 to where every XCD sees them), and the stores are complete (vmcnt 0)
-// before the segment counts itself, so the last count finds every partial.
+// partial row is stored, and the rows' partials are read back, with
+// agent-scope atomic stores and loads (sc1: past this XCD's L2, to where
+// every XCD sees them), and a segment's stores are complete (vmcnt 0) before
+// it counts itself, so the last count of a row finds all its partials.
 __device__ __forceinline__ void store_partial(float* dst, f4 v) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) __hip_atomic_store(dst + i, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -599,43 +675,59 @@ __device__ __forceinline__ void store_partial(float* dst, float v) {
   __hip_atomic_store(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Column `col` of a row's n partial rows at `base`, added in the combine's
-// order for P lane groups (combine_kernel: group q sums partials q, q + P,
-// ... in turn from zero, then the groups are added pairwise, xor 1, 2, 4),
-// so a fused row is bit for bit the combined one.  One column and one
-// partial at a time keeps the registers this cold path adds to the main
-// kernels few.
-__device__ __forceinline__ float strided_sum(const float* base, int q, int P, int n, long long ldp) {
-  float v = 0.0f;
-#pragma unroll 1
-  for (int k = q; k < n; k += P)
-    v += __hip_atomic_load(base + (long long)k * ldp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return v;
-}
-__device__ __forceinline__ float partial_tree(const float* base, int P, int n, long long ldp) {
-  if (P == 1) return strided_sum(base, 0, 1, n, ldp);
-  if (P == 2) return strided_sum(base, 0, 2, n, ldp) + strided_sum(base, 1, 2, n, ldp);
-  float a = strided_sum(base, 0, P, n, ldp) + strided_sum(base, 1, P, n, ldp);
-  a = a + (strided_sum(base, 2, P, n, ldp) + strided_sum(base, 3, P, n, ldp));
-  if (P == 4) return a;
-  float b = strided_sum(base, 4, P, n, ldp) + strided_sum(base, 5, P, n, ldp);
-  b = b + (strided_sum(base, 6, P, n, ldp) + strided_sum(base, 7, P, n, ldp));
-  return a + b;
+// sum_strided over the partial rows of one split row through a buffer
+// resource on them, with agent-scope coherent (sc1) loads: the same adds in
+// the same order.  Byte offsets fit 31 bits (launch_rowgroup_all fuses only
+// when the whole partial buffer does).
+constexpr int kCpolSc1 = 16;  // the sc1 cache-policy bit of buffer instructions
+template <int NG>
+__device__ __forceinline__ f4 sum_strided_coh(__amdgpu_buffer_rsrc_t rsrc, int c, int n, int q, long long ldp,
+                                              bool cv) {
+  f4 acc = Vec<4>::zero();
+  if (!cv) return acc;
+  auto part = [&](int k) -> f4 {
+    const int off = (int)(((long long)k * ldp + c) * 4);
+    return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, kCpolSc1));
+  };
+  int k = q;
+  for (; k + 3 * NG < n; k += 4 * NG) {
+    f4 a[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) a[u] = part(k + u * NG);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc = add_v(acc, a[u]);
+  }
+  for (; k < n; k += NG) acc = add_v(acc, part(k));
+  return acc;
 }
 
-// The whole of a split row from its n partial rows at `base` (every
-// column; C row at crow), by the G lanes of the group whose segment counted
-// last.  P follows the combine's lane groups for this N (launch_combine:
-// ceil(N / 4) float4 chunks in groups of 8, 16, 32 or 64 lanes); the
-// epilogue is the combine's, element by element.
-__device__ __forceinline__ void fused_row_sum(float* crow, const float* base, int n, long long ldp, int N,
-                                              int epi, float alpha, float beta, int gl, int G) {
-  const int chunks = (N + 3) / 4;
-  const int P = chunks <= 8 ? 8 : chunks <= 16 ? 4 : chunks <= 32 ? 2 : 1;
-#pragma unroll 1
-  for (int c = gl; c < N; c += G) {
-    const float v = partial_tree(base + c, P, n, ldp);
-    st_c(crow + c, epi1(epi, alpha, beta, v, crow + c));
+// The split rows that this wave's groups counted last (lanes in `pend`, each
+// holding row, segments n and first position x0), one after another with
+// the whole wave, in the combine's lane layout and order (combine_kernel's
+// slot scan: GC lanes a float4 chunk, 64 / GC groups adding strided
+// partials, then the xor tree), so a fused row is bit for bit the combined
+// one.
+template <int VEC, int GC>
+__device__ __forceinline__ void fused_rows(const Problem& p, unsigned long long pend, int row, int n, int x0) {
+  constexpr int P = 64 / GC;
+  const int lane = lane_id();
+  const int q = lane / GC;
+  const int gl = lane & (GC - 1);
+  while (pend) {
+    const int l = __ffsll((long long)pend) - 1;
+    pend &= pend - 1;
+    const int r = __builtin_amdgcn_readlane(row, l);
+    const int nn = __builtin_amdgcn_readlane(n, l);
+    float* base = p.partials + (long long)(__builtin_amdgcn_readlane(x0, l) >> p.seg_shift) * p.ldp;
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(base, (short)0, (int)((long long)nn * p.ldp * 4), 0x00020000);
+    float* crow = p.C + (long long)r * p.ldc;
+    for (int c0 = 0; c0 < p.N; c0 += GC * 4) {
+      const int c = c0 + gl * 4;
+      const bool cv = c < p.N;
+      const f4 acc = wave_group_sum<GC>(sum_strided_coh<P>(rsrc, c, nn, q, p.ldp, cv));
+      if (q == 0 && cv) store_cols4<VEC>(p, crow + c, c, acc);
+    }
   }
 }
 
@@ -651,9 +743,9 @@ __device__ __forceinline__ void rowgroup_block(const Problem& p, int bid, int se
   constexpr int PW = G * VEC * T;
   if (bid < seg_blocks) {
     // Long-row segments, one slot per group (grid-strided if the segment
-    // blocks are capped).  FUSE: the last segment of a split row to finish
-    // (in every column slice) notes the row in fuse_row, and its group sums
-    // the row once the gathers are done.
+    // blocks are capped).  FUSE: the group whose segment of a split row
+    // counts last (over every column slice) notes the row in fuse_row, and
+    // once the gathers are done its wave sums the rows its groups noted.
     constexpr int US = SU > U ? (SU < G ? SU : G) : U;
     auto slot = [&](int s, int& fuse_row, int& fuse_n, int& fuse_x0) {
       const int2 si = p.seg_info[s];
@@ -722,9 +814,20 @@ __device__ __forceinline__ void rowgroup_block(const Problem& p, int bid, int se
       // (launch_rowgroup_all)
       const int s = bid * GPB + gid;
       if (s < p.nslots) slot(s, fuse_row, fuse_n, fuse_x0);
-      if (fuse_row >= 0)
-        fused_row_sum(p.C + (long long)fuse_row * p.ldc, p.partials + (long long)(fuse_x0 >> p.seg_shift) * p.ldp,
-                      fuse_n, p.ldp, p.N, p.epi, p.alpha, p.beta, gl, G);
+      // the whole wave, its groups' rows one after another (GC as launch_combine picks it)
+      const unsigned long long pend = __ballot(fuse_row >= 0 && gl == 0);
+      if (pend) {
+        const int chunks = (p.N + 3) / 4;
+        if (chunks <= 8) {
+          fused_rows<VEC, 8>(p, pend, fuse_row, fuse_n, fuse_x0);
+        } else if (chunks <= 16) {
+          fused_rows<VEC, 16>(p, pend, fuse_row, fuse_n, fuse_x0);
+        } else if (chunks <= 32) {
+          fused_rows<VEC, 32>(p, pend, fuse_row, fuse_n, fuse_x0);
+        } else {
+          fused_rows<VEC, 64>(p, pend, fuse_row, fuse_n, fuse_x0);
+        }
+      }
     } else {
       for (int s = bid * GPB + gid; s < p.nslots; s += seg_blocks * GPB) slot(s, fuse_row, fuse_n, fuse_x0);
     }
@@ -1323,81 +1426,6 @@ __global__ __launch_bounds__(kWaves * 64) void share_kernel(Problem p, int share
   }
 }
 
-// Partials k = q, q + NG, q + 2*NG, ... (k < n) of one lane's four columns,
-// added in that order; partial k sits at src + idx(k) * ldp, idx(k) =
-// pieces[k] when a piece list is given, else k.  Partial rows are ldp = N
-// rounded up to 4 floats long and 256-byte aligned, so they are read as
-// float4 whatever the alignment of C.
-template <int NG>
-__device__ __forceinline__ f4 sum_strided(const float* src, const int* pieces, int n, int q,
-                                          long long ldp, bool cv) {
-  f4 acc = Vec<4>::zero();
-  if (!cv) return acc;
-  auto part = [&](int k) -> f4 {
-    const long long idx = pieces ? (long long)pieces[k] : (long long)k;
-    return *reinterpret_cast<const f4*>(src + idx * ldp);
-  };
-  int k = q;
-  for (; k + 7 * NG < n; k += 8 * NG) {
-    f4 a[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) a[u] = part(k + u * NG);
-#pragma unroll
-    for (int u = 0; u < 8; ++u) acc = add_v(acc, a[u]);
-  }
-  for (; k < n; k += NG) acc = add_v(acc, part(k));
-  return acc;
-}
-
-// The value of lane (this lane ^ OFF), OFF in {8, 16, 32}: a DPP row_ror:8
-// (rotating a 16-lane row by half of it is the xor), a ds_swizzle swapping the
-// 16-lane halves of each 32-lane group (bit mode: and 0x1f, xor 0x10), and a
-// ds_bpermute across the 32-lane halves, which no gfx9 DPP or swizzle crosses.
-template <int OFF>
-__device__ __forceinline__ float lane_xor(float v) {
-  const int x = __builtin_bit_cast(int, v);
-  int y;
-  if constexpr (OFF == 8) {
-    y = __builtin_amdgcn_update_dpp(0, x, 0x128 /* row_ror:8 */, 0xF, 0xF, false);
-  } else if constexpr (OFF == 16) {
-    y = __builtin_amdgcn_ds_swizzle(x, 0x401F);
-  } else {
-    static_assert(OFF == 32, "lane_xor: offsets 8, 16, 32");
-    y = __builtin_amdgcn_ds_bpermute((lane_id() ^ 32) << 2, x);
-  }
-  return __builtin_bit_cast(float, y);
-}
-
-template <int OFF>
-__device__ __forceinline__ f4 add_lane_xor(f4 v) {
-  return f4{v.x + lane_xor<OFF>(v.x), v.y + lane_xor<OFF>(v.y), v.z + lane_xor<OFF>(v.z),
-            v.w + lane_xor<OFF>(v.w)};
-}
-
-// Sum over the 64 / GC lane groups of a wave by a fixed xor tree (offsets GC,
-// 2 GC, ... 32); every group ends with the total.  All lanes take part.
-template <int GC>
-__device__ __forceinline__ f4 wave_group_sum(f4 v) {
-  static_assert(GC == 8 || GC == 16 || GC == 32 || GC == 64, "group widths of the combine");
-  if constexpr (GC <= 8) v = add_lane_xor<8>(v);
-  if constexpr (GC <= 16) v = add_lane_xor<16>(v);
-  if constexpr (GC <= 32) v = add_lane_xor<32>(v);
-  return v;
-}
-
-// Columns c .. c + 3 of a C row (those below N): one float4 store when C
-// rows are 16-byte aligned (VEC == 4, N % 4 == 0), else one per column.
-template <int VEC>
-__device__ __forceinline__ void store_cols4(const Problem& p, float* cptr, int c, f4 v) {
-  if constexpr (VEC == 4) {
-    store_epi<4>(p, cptr, v);
-  } else {
-    store_epi<1>(p, cptr, v.x);
-    if (c + 1 < p.N) store_epi<1>(p, cptr + 1, v.y);
-    if (c + 2 < p.N) store_epi<1>(p, cptr + 2, v.z);
-    if (c + 3 < p.N) store_epi<1>(p, cptr + 3, v.w);
-  }
-}
 
 // Table slots one wave of the combine scan reads at once.  A split row (two
 // segments or more) owns two slots or more, so a wave meets at most
@@ -1793,11 +1821,15 @@ static hipError_t launch_rowgroup_all(const Problem& p_in, int vec, bool lds, hi
   // are not capped); a stored plan has no per-call plan_kernel to zero the
   // counters, and keeps the combine.  Measured on MI355X per call (rocprof
   // sums, bit-identical to the combine): medium 49.4 -> 44.6 us (the combine
-  // launch, which found no split row, gone), large 300.4 -> 300.0 us.
+  // launch, which found no split row, gone), large 300.4 -> 300.0 us; XL
+  // without its column panels (thousands of split rows) 645 -> 654 us.  The
+  // rows' sums one lane group at a time, with a load in flight, had cost
+  // that call 58 us.
   Problem p = p_in;
   p.seg_fuse = CSRSPMM_SEG_FUSE && p.plan && !p.plan_ready && p.nslots > 0 && !p.no_split && !p.shares &&
                p.npan == 0 && p.dp.P == 0 && p.seg_cnt != nullptr &&
-               (long long)p.nslots <= (long long)kSegBlocksMax * kWaves;
+               (long long)p.nslots <= (long long)kSegBlocksMax * kWaves &&
+               (long long)(p.nnz >> p.seg_shift) * p.ldp * 4 < (1LL << 31);
   if (p.plan && !p.plan_ready) hipLaunchKernelGGL(plan_kernel, dim3(plan_blocks(p)), dim3(256), 0, s, p);
   hipError_t e;
   if (p.dp.P > 0 && !p.dp_ready) {
