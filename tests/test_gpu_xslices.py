@@ -9,11 +9,12 @@ cases: two and four bands, a last partial band (N = 124), long rows on
 segments and the combine, the beta epilogue, a stored plan, and the scalar
 variants on the same shapes (which keep the unsliced path).
 
-Combine early exit: plan_kernel flags each of its row blocks (256 rows,
-grid-strided past 4096 blocks) holding a row that needs the combine; the
-combine returns at once when none does.  The cases put a single long row in
-the first, a middle and the last row block, and in a grid-strided block of
-a matrix of over 2^20 rows.
+A single long row: plan_kernel handles rows in blocks of 256 (grid-strided
+past 4096 blocks), zeroing each split row's segment counter and flagging
+its block for the combine of a stored plan; per call the row is summed in
+the main launch by the wave whose segment counts last.  The cases put the
+row in the first, a middle and the last row block, and in a grid-strided
+block of a matrix of over 2^20 rows.
 
 Bar: 1e-5 against the fp64 oracle on every element; rows summed whole
 (csr_cases.whole_row_max) bit for bit against the fp32 restatement.
@@ -95,8 +96,8 @@ def test_xslices_short_rows_epilogue(algo, gpu):
 @pytest.mark.parametrize("where", ["first", "middle", "last", "strided"])
 @pytest.mark.parametrize("algo", ["WarpPerRow", "WarpPerRowFp4", "WarpPerRowSmemFp4"])
 def test_combine_single_long_row(algo, where, gpu):
-    """One row of 3000 nonzeros among rows of 0-3: only its plan row block
-    is flagged for the combine."""
+    """One row of 3000 nonzeros among rows of 0-3, split into segments and
+    summed in the main launch."""
     K, N = 4096, 64
     M = 1_100_000 if where == "strided" else 60000
     rng = np.random.default_rng(9)
