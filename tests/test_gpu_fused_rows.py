@@ -15,7 +15,9 @@ the segment shrinks (to 32 at the smallest), so rows of a few hundred
 nonzeros split into many segments.  Cases: unsliced float4 and scalar
 columns, XCD slices (16384 x 128), column slices launched one by one (K =
 65536, N = 256: a row's segments count over four slices), the alpha/beta
-epilogue, and two calls in a row (the counters start from zero each call).
+epilogue, N = 1 (the combine's 8-lane groups, eight strided sums) and
+N = 600 (64-lane groups, one sum over every partial), and two calls in a row
+(the counters start from zero each call).
 
 Bar: 1e-5 against the fp64 oracle on every element; split rows bit for bit
 between the per-call and the stored-plan products.
@@ -56,7 +58,7 @@ def per_call(algo, rp, ci, va, B, dev, C0, alpha, beta):
 
 
 @pytest.mark.parametrize("M,K,N", [(4000, 4096, 64), (3000, 16384, 128), (2500, 65536, 256),
-                                   (3000, 8192, 36)])
+                                   (3000, 8192, 36), (3000, 4096, 1), (1500, 4096, 600)])
 @pytest.mark.parametrize("algo", VARIANTS)
 def test_fused_split_rows(algo, M, K, N, gpu):
     lens = lengths(M, seed=K + N)
