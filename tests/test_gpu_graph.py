@@ -9,7 +9,9 @@ the in-place forms, new C values) written eagerly between the replays, every
 replay checked bit for bit against an eager call on the same inputs and the
 last one against the fp64 oracle at the 1e-5 bar.  The shapes take every
 launch of the per-call path: the plan, the column-panel schedule (a 64 MiB
-B with rows of thousands of nonzeros), the main launch and the combine."""
+B with rows of thousands of nonzeros), the main launch and the combine, and
+split rows summed in the main launch (their counters zeroed by plan_kernel
+in every replay)."""
 import numpy as np
 import pytest
 import torch
@@ -35,6 +37,12 @@ def cases():
     lens = rng.integers(0, 40, size=20000)
     rp, ci, va = csr_from_lengths(lens, 4096, seed=92)
     yield "short", rp, ci, va, 4096, 96
+    # rows split into segments on a B without panels or XCD shares: summed in
+    # the main launch, their counters zeroed by plan_kernel on every replay
+    lens = rng.integers(0, 30, size=6000)
+    lens[rng.choice(6000, 600, replace=False)] = rng.integers(300, 1000, size=600)
+    rp, ci, va = csr_from_lengths(lens, 4096, seed=93)
+    yield "split", rp, ci, va, 4096, 64
 
 
 CASES = list(cases())
