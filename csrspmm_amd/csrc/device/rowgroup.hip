@@ -927,6 +927,8 @@ __device__ __forceinline__ void interleave_roles(int b, int piece_blocks, int to
 // column panels).  The kernels of calls without them are compiled without
 // that code, which as dead code cost the scalar N <= 64 kernel 9% on R-MAT
 // and the scalar N = 128 / 256 kernels 3-18% on the reference's sweep shapes.
+// FUSE: the segment blocks sum the split rows themselves (Problem::seg_fuse),
+// in instances of their own, so that the other kernels keep their registers.
 template <int VEC, int G, int T, int U, bool LDS, bool PIECES, int SU, bool BUF, bool SWEEP, bool FUSE = false>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(SWEEP ? CSRSPMM_SWEEP_WPE : 1))) void rowgroup_kernel(Problem p, int piece_blocks,
                                                                 int seg_blocks, int slice_blocks,
@@ -1580,6 +1582,7 @@ void launch_combine(const Problem& p, hipStream_t s) {
 // SU: B-row gathers in flight per lane in the long-row segments (at least U).
 // BUF: B gathered through a buffer resource (buf_gathers_ok must hold).
 // SWEEP: the short rows of each slice in a band sweep (p.sweep_bands > 0).
+// p.seg_fuse launches the FUSE instance of the kernel without pieces.
 template <int VEC, int G, int T, int U, bool LDS, int SU = CSRSPMM_SEG_UNROLL, bool BUF = false,
           bool SWEEP = false>
 hipError_t launch_rg(const Problem& p, hipStream_t s) {
